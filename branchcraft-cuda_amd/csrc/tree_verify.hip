@@ -1,0 +1,499 @@
+// Ancestor-only tree verification over a shared paged prefix for gfx950.
+//
+// Reference: tree_kernel / tree_verify (src/tree_attention.cu:14-71,
+// 93-105).  The reference gives every (request, node, query head) one warp
+// that walks the whole prefix token by token.  Here the query rows of one KV
+// head -- nodes x GQA group, e.g. 7 x 4 = 28 -- fill the 32 columns of a
+// v_mfma_f32_32x32x16_f16 tile, so each K/V token is read once per request
+// and KV head and serves every candidate:
+//
+//   S^T[32 tok x 32 rows] = K[32 tok x D] . Q^T[D x 32 rows]   (D/16 MFMAs)
+//   O^T[D x 32 rows]     += V^T[D x 32 tok] . P^T[32 tok x 32 rows]
+//
+// K tiles feed the A operand straight from HBM (16 contiguous bytes per lane
+// per MFMA).  The S^T accumulator layout is, lane for lane, the B operand of
+// the P.V product once the token order inside a 16-token step is permuted
+// (token tau(s,g,i) = 16s + 8*(i/4) + 4g + i%4 for lane half g), so P never
+// leaves registers.  V is staged row-major in LDS (per wave, 32 tokens x D,
+// one 16-byte store per lane and k-step) and the V^T A operand is read with
+// ds_read_b64_tr_b16: inside each 16-lane group, lane i receives element
+// i%4 of the 8-byte chunks addressed by lanes i/4 + 4k (k = 0..3), so lanes
+// that address [token tb + j/4][dim db + 4*(j%4)] yield V[tb + k][db + i].  The draft nodes form
+// extra 32-token tiles whose scores are masked by the row's ancestor set,
+// walked from the parent array held in LDS (at most N steps, stopping at a
+// parent outside [0, N)).
+//
+// Work unit: (request, KV head, row tile, prefix chunk).  Four waves take
+// 32-token tiles round-robin and merge their online-softmax states through
+// LDS; with a workspace, chunks write FP32 partials that merge_tree_kernel
+// combines.  Workgroup ids put (KV head, row tile) in the low bits, so the
+// requests that share prefix pages run on the same XCD and reuse its L2.
+#include "bc_device.h"
+
+namespace {
+
+using namespace bcd;
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kWaves = 4;
+constexpr int kThreads = 64 * kWaves;
+constexpr int kTile = 32;       // tokens per MFMA tile (two pages)
+// Halves per staged V row: D + 32 spaces the four token rows a 16-lane
+// transpose read touches 16 banks apart.
+template <int D>
+constexpr int v_pitch() { return D + 32; }
+
+struct TreeParams {
+  const uint16_t* k;        // prefix K [P,16,Hkv,D]
+  const uint16_t* v;        // prefix V
+  const int32_t* pages;     // [B, max_pages]
+  const int32_t* lengths;   // [B]
+  const uint16_t* dq;       // draft Q [B,N,Hq,D]
+  const uint16_t* dk;       // draft K [B,N,Hkv,D]
+  const uint16_t* dv;       // draft V
+  const int32_t* parent;    // [B,N]
+  float* out;               // [B,N,Hq,D]
+  float* part_acc;          // workspace partials (null: one unit per row tile)
+  float* part_ml;
+  int batch, nodes, hq, hkv, group, max_pages, phys_pages;
+  int rows, row_tiles;      // rows = nodes * group per (request, KV head)
+  int chunk_tokens;         // prefix tokens per chunk (workspace mode)
+  int prefix_parts;         // chunk slots per row; slot prefix_parts = drafts
+  float scale_log2;
+};
+
+__device__ __forceinline__ f16x8 as_f16x8(const uint4 u) {
+  return __builtin_bit_cast(f16x8, u);
+}
+
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ f16x4 lds_read_tr(const _Float16* p) {
+  const i16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) i16x4*)(p));
+  return __builtin_bit_cast(f16x4, r);
+}
+
+__device__ __forceinline__ size_t slot_index(const TreeParams& P, int b,
+                                             int node, int h, int part) {
+  return (((size_t)b * P.nodes + node) * P.hq + h) * (P.prefix_parts + 1) + part;
+}
+
+template <int D>
+__global__ __launch_bounds__(kThreads) void tree_kernel(TreeParams P) {
+  constexpr int KS = D / 16;  // MFMA k-steps over the head dimension
+  constexpr int DT = D / 32;  // 32-row output tiles over the head dimension
+  constexpr int VP = v_pitch<D>();
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int g = lane >> 5;   // lane half
+  const int lr = lane & 31;  // tile column (query row) / token slot
+
+  const int zdim = P.hkv * P.row_tiles;
+  const int z = blockIdx.x % zdim;
+  const int b = (blockIdx.x / zdim) % P.batch;
+  const int part = blockIdx.x / (zdim * P.batch);
+  const int kvh = z / P.row_tiles;
+  const int rt = z % P.row_tiles;
+
+  const int len = max(0, min(P.lengths[b], P.max_pages * BC_PAGE_SIZE));
+  int pbeg = 0, pend = len;
+  bool drafts = true, final_out = true;
+  if (P.part_acc) {
+    const int nparts = (len + P.chunk_tokens - 1) / P.chunk_tokens;
+    if (part < P.prefix_parts) {
+      if (part >= nparts) return;  // uniform over the workgroup
+      pbeg = part * P.chunk_tokens;
+      pend = min(pbeg + P.chunk_tokens, len);
+      drafts = false;
+    } else {
+      pend = 0;
+    }
+    final_out = nparts == 0;
+  }
+  const int tp0 = pbeg / kTile;
+  const int ntile_p = pend > pbeg ? (pend - 1) / kTile - tp0 + 1 : 0;
+  const int ntile_d = drafts ? (P.nodes + kTile - 1) / kTile : 0;
+
+  // This lane's query row (tile column lr).
+  const int r = rt * 32 + lr;
+  const bool rvalid = r < P.rows;
+  const int node = rvalid ? r / P.group : 0;
+  const int h = kvh * P.group + (rvalid ? r % P.group : 0);
+  uint4 qreg[KS];
+  {
+    const uint16_t* qp = P.dq + (((size_t)b * P.nodes + node) * P.hq + h) * D + 8 * g;
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+      qreg[s] = rvalid ? ldg16(qp + 16 * s) : make_uint4(0, 0, 0, 0);
+  }
+
+  __shared__ int s_parent[BC_MAX_TREE_NODES];
+  __shared__ __attribute__((aligned(16))) char s_mem[kWaves * kTile * VP * 2];
+  __shared__ float s_m[2][32], s_l[2][32];
+  if (drafts)
+    for (int i = threadIdx.x; i < P.nodes; i += kThreads)
+      s_parent[i] = P.parent[(size_t)b * P.nodes + i];
+  __syncthreads();
+
+  _Float16* vs = reinterpret_cast<_Float16*>(s_mem) + wave * kTile * VP;
+  // Transpose-read address of this lane: group G = lane/16, j = lane%16.
+  const int trG = lane >> 4, trj = lane & 15;
+  const _Float16* vtr = vs + (4 * (trG >> 1) + (trj >> 2)) * VP + 16 * (trG & 1) + 4 * (trj & 3);
+  f32x16 acc[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+    for (int j = 0; j < 16; ++j) acc[dt][j] = 0.f;
+  float m = kNegInf, l = 0.f;
+
+  const size_t tok_stride = (size_t)P.hkv * D;  // elements between slots
+
+  for (int it = wave; it < ntile_p + ntile_d; it += kWaves) {
+    const bool is_draft = it >= ntile_p;
+    // ---- load this lane's token row (token lr of the tile) ----
+    const uint16_t* kp;
+    const uint16_t* vp;
+    bool tv;
+    int tbase;          // first token (prefix) or first node (draft) of tile
+    bool page_ok[2] = {true, true};
+    if (!is_draft) {
+      tbase = (tp0 + it) * kTile;
+      // The two pages of the tile (uniform scalar loads).
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const int pg = tbase / BC_PAGE_SIZE + q;
+        const int phys = pg < P.max_pages ? P.pages[(size_t)b * P.max_pages + pg] : -1;
+        page_ok[q] = phys >= 0 && phys < P.phys_pages;
+      }
+      const int t = tbase + lr;
+      tv = t >= pbeg && t < pend && page_ok[lr >> 4];
+      size_t off = 0;
+      if (tv) {
+        const size_t phys = (size_t)P.pages[(size_t)b * P.max_pages + t / BC_PAGE_SIZE];
+        off = (phys * BC_PAGE_SIZE + t % BC_PAGE_SIZE) * tok_stride + (size_t)kvh * D;
+      }
+      kp = P.k + off;
+      vp = P.v + off;
+    } else {
+      tbase = (it - ntile_p) * kTile;
+      const int dn = tbase + lr;
+      tv = dn < P.nodes;
+      const size_t off = tv ? (((size_t)b * P.nodes + dn) * P.hkv + kvh) * D : 0;
+      kp = P.dk + off;
+      vp = P.dv + off;
+    }
+    uint4 kreg[KS], vreg[KS];
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      kreg[s] = tv ? ldg16(kp + 16 * s + 8 * g) : make_uint4(0, 0, 0, 0);
+      vreg[s] = tv ? ldg16(vp + 16 * s + 8 * g) : make_uint4(0, 0, 0, 0);
+    }
+
+    // ---- S^T = K Q^T ----
+    f32x16 sc;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) sc[j] = 0.f;
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+      sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_f16x8(kreg[s]),
+                                                  as_f16x8(qreg[s]), sc, 0, 0, 0);
+
+    // ---- stage V row-major while the MFMAs drain ----
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+      *reinterpret_cast<uint4*>(vs + lr * VP + 16 * s + 8 * g) = vreg[s];
+
+    // ---- mask and online softmax (column lr = query row) ----
+    uint32_t anc = 0;
+    if (is_draft) {
+      // Ancestor-or-self bits of this row's node inside draft tile tbase.
+      int cur = node;
+      for (int steps = 0; steps < P.nodes && cur >= 0 && cur < P.nodes; ++steps) {
+        if (cur >= tbase && cur < tbase + kTile) anc |= 1u << (cur - tbase);
+        cur = s_parent[cur];
+      }
+    }
+    float sv[16];
+    float tmax = kNegInf;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int tk = 8 * (j >> 2) + 4 * g + (j & 3);  // token row of sc[j]
+      bool ok;
+      if (is_draft) {
+        ok = (anc >> tk) & 1u;
+      } else {
+        const int t = tbase + tk;
+        ok = t >= pbeg && t < pend && page_ok[tk >> 4];
+      }
+      sv[j] = ok ? sc[j] * P.scale_log2 : kNegInf;
+      tmax = __builtin_fmaxf(tmax, sv[j]);
+    }
+    tmax = __builtin_fmaxf(tmax, shfl_xor_f(tmax, 32));
+    const float mnew = __builtin_fmaxf(m, tmax);
+    if (__builtin_amdgcn_ballot_w64(mnew > m)) {
+      const float alpha = fast_exp2(m - safe_max(mnew));
+      l *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) acc[dt][j] *= alpha;
+      m = mnew;
+    }
+    const float mb = safe_max(m);
+    f16x8 pb[2];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const float pr = fast_exp2(sv[j] - mb);
+      l += pr;
+      pb[j >> 3][j & 7] = (_Float16)pr;
+    }
+
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // ---- O^T += V^T P^T; A operand tokens 16st + 8hf + 4g + k, dim lr ----
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+#pragma unroll
+      for (int st = 0; st < 2; ++st) {
+        const f16x4 lo = lds_read_tr(vtr + (16 * st) * VP + 32 * dt);
+        const f16x4 hi = lds_read_tr(vtr + (16 * st + 8) * VP + 32 * dt);
+        const f16x8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pb[st], acc[dt], 0, 0, 0);
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+
+  // Both lane halves share m; combine their partial sums.
+  l += shfl_xor_f(l, 32);
+
+  // ---- merge the four waves: 3,2 -> 1,0 then 1 -> 0 through LDS ----
+  static_assert(kWaves * kTile * VP * 2 >= 2 * 32 * D * 4, "merge buffer fits");
+  float* xacc = reinterpret_cast<float*>(s_mem);  // [2][32 rows][D]
+  auto put = [&](int slot) {
+    float* dst = xacc + (size_t)slot * 32 * D + (size_t)lr * D;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int jq = 0; jq < 4; ++jq) {
+        float4 v4 = make_float4(acc[dt][4 * jq], acc[dt][4 * jq + 1],
+                                acc[dt][4 * jq + 2], acc[dt][4 * jq + 3]);
+        *reinterpret_cast<float4*>(dst + 32 * dt + 8 * jq + 4 * g) = v4;
+      }
+    if (g == 0) {
+      s_m[slot][lr] = m;
+      s_l[slot][lr] = l;
+    }
+  };
+  auto take = [&](int slot) {
+    const float* src = xacc + (size_t)slot * 32 * D + (size_t)lr * D;
+    const float m2 = s_m[slot][lr], l2 = s_l[slot][lr];
+    const float mm = __builtin_fmaxf(m, m2);
+    const float a1 = fast_exp2(m - safe_max(mm)), a2 = fast_exp2(m2 - safe_max(mm));
+    l = l * a1 + l2 * a2;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int jq = 0; jq < 4; ++jq) {
+        const float4 v4 = *reinterpret_cast<const float4*>(src + 32 * dt + 8 * jq + 4 * g);
+        acc[dt][4 * jq] = acc[dt][4 * jq] * a1 + v4.x * a2;
+        acc[dt][4 * jq + 1] = acc[dt][4 * jq + 1] * a1 + v4.y * a2;
+        acc[dt][4 * jq + 2] = acc[dt][4 * jq + 2] * a1 + v4.z * a2;
+        acc[dt][4 * jq + 3] = acc[dt][4 * jq + 3] * a1 + v4.w * a2;
+      }
+    m = mm;
+  };
+  __syncthreads();  // V^T staging area is reused below
+  if (wave >= 2) put(wave - 2);
+  __syncthreads();
+  if (wave < 2) take(wave);
+  __syncthreads();
+  if (wave == 1) put(0);
+  __syncthreads();
+  if (wave != 0) return;
+  take(0);
+  if (!rvalid) return;
+
+  // ---- write: lane holds O^T[32dt + 8jq + 4g + e][row r] ----
+  if (final_out) {
+    float* dst = P.out + (((size_t)b * P.nodes + node) * P.hq + h) * D;
+    const float inv = 1.f / l;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int jq = 0; jq < 4; ++jq)
+        *reinterpret_cast<float4*>(dst + 32 * dt + 8 * jq + 4 * g) =
+            make_float4(acc[dt][4 * jq] * inv, acc[dt][4 * jq + 1] * inv,
+                        acc[dt][4 * jq + 2] * inv, acc[dt][4 * jq + 3] * inv);
+  } else {
+    const int p = drafts ? P.prefix_parts : part;
+    const size_t slot = slot_index(P, b, node, h, p);
+    float* dst = P.part_acc + slot * D;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int jq = 0; jq < 4; ++jq)
+        *reinterpret_cast<float4*>(dst + 32 * dt + 8 * jq + 4 * g) =
+            make_float4(acc[dt][4 * jq], acc[dt][4 * jq + 1], acc[dt][4 * jq + 2],
+                        acc[dt][4 * jq + 3]);
+    if (g == 0) {
+      P.part_ml[2 * slot] = m;
+      P.part_ml[2 * slot + 1] = l;
+    }
+  }
+}
+
+// Combines the prefix chunks and the draft part of every (b, node, h).
+template <int D>
+__global__ __launch_bounds__(256) void merge_tree_kernel(TreeParams P) {
+  const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
+  const size_t total = (size_t)P.batch * P.nodes * P.hq * D;
+  if (idx >= total) return;
+  const int d = idx % D;
+  const size_t row = idx / D;  // (b*N + node)*Hq + h
+  const int b = row / ((size_t)P.nodes * P.hq);
+  const int len = max(0, min(P.lengths[b], P.max_pages * BC_PAGE_SIZE));
+  const int nparts = (len + P.chunk_tokens - 1) / P.chunk_tokens;
+  if (nparts == 0) return;  // the draft part wrote the final output
+  const size_t base = row * (P.prefix_parts + 1);
+  float mm = P.part_ml[2 * (base + P.prefix_parts)];
+  for (int p = 0; p < nparts; ++p) mm = __builtin_fmaxf(mm, P.part_ml[2 * (base + p)]);
+  float lsum = 0.f, asum = 0.f;
+  for (int p = 0; p <= nparts; ++p) {
+    const size_t s = base + (p == nparts ? P.prefix_parts : p);
+    const float w = fast_exp2(P.part_ml[2 * s] - mm);
+    lsum += w * P.part_ml[2 * s + 1];
+    asum += w * P.part_acc[s * D + d];
+  }
+  P.out[idx] = asum / lsum;
+}
+
+bool tree_args_ok(const bc_shape& s, const bc_tree_inputs& in, int nodes) {
+  return s.batch >= 1 && s.query_heads >= 1 && s.kv_heads >= 1 &&
+         s.query_heads % s.kv_heads == 0 && (s.dim == 64 || s.dim == 128) &&
+         s.max_pages >= 1 && nodes >= 1 && nodes <= BC_MAX_TREE_NODES &&
+         in.prefix.k && in.prefix.v && in.prefix.pages && in.prefix.lengths &&
+         in.draft_q && in.draft_k && in.draft_v && in.parent && in.output;
+}
+
+bool aligned16(const void* p) {
+  return (reinterpret_cast<uintptr_t>(p) & 15) == 0;
+}
+
+TreeParams make_params(const bc_shape& s, const bc_tree_inputs& in, int nodes) {
+  TreeParams P{};
+  P.k = in.prefix.k;
+  P.v = in.prefix.v;
+  P.pages = in.prefix.pages;
+  P.lengths = in.prefix.lengths;
+  P.dq = in.draft_q;
+  P.dk = in.draft_k;
+  P.dv = in.draft_v;
+  P.parent = in.parent;
+  P.out = in.output;
+  P.batch = s.batch;
+  P.nodes = nodes;
+  P.hq = s.query_heads;
+  P.hkv = s.kv_heads;
+  P.group = s.query_heads / s.kv_heads;
+  P.max_pages = s.max_pages;
+  // physical_pages is not part of the reference tree contract
+  // (bindings/torch_ops.cpp:54 passes prefix_k.size(0)); 0 means unchecked.
+  P.phys_pages = s.physical_pages >= 1 ? s.physical_pages : 0x7fffffff;
+  P.rows = nodes * P.group;
+  P.row_tiles = (P.rows + 31) / 32;
+  P.scale_log2 = (float)(1.4426950408889634 / __builtin_sqrt((double)s.dim));
+  return P;
+}
+
+// Prefix chunking for the workspace path: enough workgroups to cover the
+// 256 CUs about twice, chunks of at least 128 tokens, multiples of 32.
+void tree_chunking(const bc_shape& s, int nodes, int* chunk_tokens, int* parts) {
+  const int group = s.query_heads / s.kv_heads;
+  const long long units =
+      (long long)s.batch * s.kv_heads * ((nodes * group + 31) / 32);
+  const int max_tokens = s.max_pages * BC_PAGE_SIZE;
+  long long want = (512 + units - 1) / units;
+  if (want < 1) want = 1;
+  int chunk = (int)((max_tokens + want - 1) / want);
+  chunk = (chunk + kTile - 1) / kTile * kTile;
+  if (chunk < 128) chunk = 128;
+  *chunk_tokens = chunk;
+  *parts = (max_tokens + chunk - 1) / chunk;
+}
+
+size_t tree_workspace(const bc_shape& s, int nodes, int* chunk_tokens, int* parts) {
+  tree_chunking(s, nodes, chunk_tokens, parts);
+  if (*parts <= 1) return 0;
+  const size_t slots = (size_t)s.batch * nodes * s.query_heads * (*parts + 1);
+  const size_t acc = (slots * s.dim * sizeof(float) + 255) & ~(size_t)255;
+  return acc + slots * 2 * sizeof(float);
+}
+
+hipError_t launch_tree(TreeParams& P, int dim, int parts, hipStream_t st) {
+  const dim3 grid((unsigned)((size_t)parts * P.batch * P.hkv * P.row_tiles));
+  if (dim == 64) tree_kernel<64><<<grid, kThreads, 0, st>>>(P);
+  else tree_kernel<128><<<grid, kThreads, 0, st>>>(P);
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess || !P.part_acc) return err;
+  const size_t n = (size_t)P.batch * P.nodes * P.hq * dim;
+  const dim3 mgrid((unsigned)((n + 255) / 256));
+  if (dim == 64) merge_tree_kernel<64><<<mgrid, 256, 0, st>>>(P);
+  else merge_tree_kernel<128><<<mgrid, 256, 0, st>>>(P);
+  return hipGetLastError();
+}
+
+bool tree_ptrs_aligned(const bc_tree_inputs& in) {
+  return aligned16(in.prefix.k) && aligned16(in.prefix.v) &&
+         aligned16(in.draft_q) && aligned16(in.draft_k) &&
+         aligned16(in.draft_v) && aligned16(in.output);
+}
+
+}  // namespace
+
+extern "C" int bc_tree_verify(bc_shape s, bc_tree_inputs in, int nodes,
+                              bc_stream_t stream) {
+  if (!tree_args_ok(s, in, nodes) || !tree_ptrs_aligned(in))
+    return BC_ERROR_INVALID_VALUE;
+  TreeParams P = make_params(s, in, nodes);
+  P.prefix_parts = 0;
+  return launch_tree(P, s.dim, 1, reinterpret_cast<hipStream_t>(stream));
+}
+
+extern "C" size_t bc_tree_verify_workspace_size(bc_shape s, int nodes) {
+  bc_tree_inputs dummy{};
+  (void)dummy;
+  if (s.batch < 1 || s.query_heads < 1 || s.kv_heads < 1 ||
+      s.query_heads % s.kv_heads || (s.dim != 64 && s.dim != 128) ||
+      s.max_pages < 1 || nodes < 1 || nodes > BC_MAX_TREE_NODES)
+    return 0;
+  int chunk = 0, parts = 0;
+  return tree_workspace(s, nodes, &chunk, &parts);
+}
+
+extern "C" int bc_tree_verify_ws(bc_shape s, bc_tree_inputs in, int nodes,
+                                 void* workspace, size_t workspace_bytes,
+                                 bc_stream_t stream) {
+  if (!tree_args_ok(s, in, nodes) || !tree_ptrs_aligned(in))
+    return BC_ERROR_INVALID_VALUE;
+  int chunk = 0, parts = 0;
+  const size_t need = tree_workspace(s, nodes, &chunk, &parts);
+  if (!workspace || need == 0 || workspace_bytes < need)
+    return bc_tree_verify(s, in, nodes, stream);
+  TreeParams P = make_params(s, in, nodes);
+  P.chunk_tokens = chunk;
+  P.prefix_parts = parts;
+  const size_t slots = (size_t)s.batch * nodes * s.query_heads * (parts + 1);
+  const size_t acc = (slots * s.dim * sizeof(float) + 255) & ~(size_t)255;
+  P.part_acc = static_cast<float*>(workspace);
+  P.part_ml = reinterpret_cast<float*>(static_cast<char*>(workspace) + acc);
+  return launch_tree(P, s.dim, parts + 1, reinterpret_cast<hipStream_t>(stream));
+}

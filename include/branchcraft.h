@@ -1,0 +1,179 @@
+/*
+ * Branchcraft paged-attention hot path for MI355X (gfx950): the C ABI.
+ *
+ * Every entry point takes plain device pointers, POD structs and a HIP
+ * stream, launches asynchronously on that stream and never synchronises or
+ * allocates.  Return values are HIP error codes: BC_SUCCESS (hipSuccess) or
+ * BC_ERROR_INVALID_VALUE (hipErrorInvalidValue) when an argument check
+ * fails, otherwise the launch error reported by the HIP runtime.
+ *
+ * FP16 tensors are passed as `const bc_half*` (IEEE binary16 bit patterns).
+ * The library holds no global state and is reentrant.
+ *
+ * Reference interface replaced: include/branchcraft.hpp:8-74 of
+ * Haaziq386/branchcraft-cuda (namespace branchcraft, cudaError_t returns).
+ */
+#ifndef BRANCHCRAFT_H_
+#define BRANCHCRAFT_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef uint16_t bc_half;
+/* Same type as hipStream_t; a null stream is the default stream. */
+typedef struct ihipStream_t* bc_stream_t;
+
+enum {
+  BC_SUCCESS = 0,             /* hipSuccess */
+  BC_ERROR_INVALID_VALUE = 1, /* hipErrorInvalidValue */
+};
+
+/* Tokens per KV page (reference: kPageSize, include/branchcraft.hpp:8). */
+#define BC_PAGE_SIZE 16
+/* Largest split count bc_decode accepts (the reference caps at 16,
+ * src/paged_gqa.cu:126; the cap is raised here, scratch stays caller-sized). */
+#define BC_MAX_SPLITS 256
+/* Largest draft tree (reference: src/tree_attention.cu:96). */
+#define BC_MAX_TREE_NODES 256
+
+/* Reference: struct Shape, include/branchcraft.hpp:11-18 (same field order). */
+typedef struct bc_shape {
+  int batch;
+  int query_heads;
+  int kv_heads;
+  int dim;            /* 64 or 128 */
+  int max_pages;      /* page-table row length */
+  int physical_pages; /* pool size P */
+} bc_shape;
+
+/* Reference: struct Inputs, include/branchcraft.hpp:20-30.
+ * q [B,Hq,D] f16; k, v [P,16,Hkv,D] f16; pages [B,max_pages] i32;
+ * lengths [B] i32; output [B,Hq,D] f32.  Empty sequences produce zeros. */
+typedef struct bc_inputs {
+  const bc_half* q;
+  const bc_half* k;
+  const bc_half* v;
+  const int32_t* pages;
+  const int32_t* lengths;
+  float* output;
+} bc_inputs;
+
+/* Reference: struct Scratch, include/branchcraft.hpp:32-37.
+ * For splits > 1 the caller provides partial_a = splits*B*Hq*D floats and
+ * partial_ml = splits*B*Hq*2 floats; both may be null for splits == 1. */
+typedef struct bc_scratch {
+  float* partial_a;
+  float* partial_ml;
+} bc_scratch;
+
+/* Reference: struct TreeInputs, include/branchcraft.hpp:43-53.
+ * draft_q [B,N,Hq,D]; draft_k/draft_v [B,N,Hkv,D]; parent [B,N] with
+ * parent < node or -1; output f32 [B,N,Hq,D].  prefix.q and prefix.output
+ * are unused and may be null. */
+typedef struct bc_tree_inputs {
+  bc_inputs prefix;
+  const bc_half* draft_q;
+  const bc_half* draft_k;
+  const bc_half* draft_v;
+  const int32_t* parent;
+  float* output;
+} bc_tree_inputs;
+
+/* Paged GQA decode with `splits` equal partitions per sequence and an FP32
+ * merge of the partial softmax states.
+ * Replaces branchcraft::decode, include/branchcraft.hpp:39-40
+ * (src/paged_gqa.cu:198-208).  Rejects: batch/Hq/Hkv < 1, Hq % Hkv != 0,
+ * dim not 64/128, max_pages or physical_pages < 1, splits outside
+ * [1, BC_MAX_SPLITS], a null input, null scratch with splits > 1. */
+int bc_decode(bc_shape shape, bc_inputs in, bc_scratch scratch, int splits,
+              bc_stream_t stream);
+
+/* Split-count heuristic for bc_decode on a device with `cu_count` compute
+ * units.  Replaces branchcraft::auto_splits, include/branchcraft.hpp:41
+ * (src/paged_gqa.cu:210-218); retuned for 256-CU MI355X workgroups. */
+int bc_auto_splits(bc_shape shape, int max_length, int cu_count);
+
+/* Ancestor-only tree verification over a paged prefix.
+ * Replaces branchcraft::tree_verify, include/branchcraft.hpp:55-56
+ * (src/tree_attention.cu:93-105).  Runs without scratch: one workgroup
+ * per (request, KV head, row tile) streams the whole prefix. */
+int bc_tree_verify(bc_shape shape, bc_tree_inputs in, int nodes,
+                   bc_stream_t stream);
+
+/* Bytes of workspace bc_tree_verify_ws needs for this shape (0 when the
+ * shape does not benefit from splitting the prefix). */
+size_t bc_tree_verify_workspace_size(bc_shape shape, int nodes);
+
+/* bc_tree_verify with the prefix split into chunks across workgroups and an
+ * FP32 merge; `workspace` holds at least bc_tree_verify_workspace_size
+ * bytes (256-byte aligned).  A null workspace or workspace_bytes smaller
+ * than required falls back to bc_tree_verify.  Results match
+ * bc_tree_verify within floating-point reassociation. */
+int bc_tree_verify_ws(bc_shape shape, bc_tree_inputs in, int nodes,
+                      void* workspace, size_t workspace_bytes,
+                      bc_stream_t stream);
+
+/* Copy accepted draft K/V rows into physical cache slots:
+ * cache[dest_pages[i], dest_slots[i]] <- draft[request, path_nodes[i]] for
+ * i < accepted, K and V, bit-exact.  Entries whose node, page or slot is out
+ * of range are skipped.  shape.kv_heads, shape.dim, shape.batch and
+ * shape.physical_pages describe the tensors.
+ * Replaces branchcraft::commit_path, include/branchcraft.hpp:61-65
+ * (src/tree_attention.cu:107-122). */
+int bc_commit_path(bc_shape shape, const bc_half* draft_k,
+                   const bc_half* draft_v, bc_half* cache_k, bc_half* cache_v,
+                   const int32_t* path_nodes, const int32_t* dest_pages,
+                   const int32_t* dest_slots, int request, int nodes,
+                   int accepted, bc_stream_t stream);
+
+/* Copy whole pages (all 16 slots, K and V) cache[dst_pages[i]] <-
+ * cache[src_pages[i]] for i < count: the copy-on-write clone of a shared
+ * partial page.  Out-of-range page ids are skipped.  No reference C++
+ * counterpart: it replaces the D2D copies at src/main.cu:276-281 and the
+ * torch copy_ at python/branchcraft_torch/transaction.py:133-134. */
+int bc_copy_pages(bc_shape shape, bc_half* cache_k, bc_half* cache_v,
+                  const int32_t* src_pages, const int32_t* dst_pages,
+                  int count, bc_stream_t stream);
+
+/* vLLM-style packed-cache decode with FP16 output.  Token t of sequence b
+ * lives at element offset
+ *   pages[b, t/16]*block_stride + kvh*head_stride + (t%16)*slot_stride
+ * with K at that offset and V at offset + kv_stride; the head dimension is
+ * contiguous.  kv_stride == dim gives the reference's logical
+ * [P,Hkv,16,2D] layout; [P,2,16,Hkv,D] uses kv_stride = 16*Hkv*D.
+ * Replaces branchcraft::packed_decode, include/branchcraft.hpp:70-74
+ * (src/packed_decode.cu:188-206), adding kv_stride.  Rejects the bc_decode
+ * shape rules plus any stride < 1 and scale <= 0 (or NaN). */
+int bc_packed_decode(bc_shape shape, const bc_half* q, const bc_half* packed_kv,
+                     const int32_t* pages, const int32_t* lengths,
+                     bc_half* output, long long block_stride,
+                     long long head_stride, long long slot_stride,
+                     long long kv_stride, float scale, bc_stream_t stream);
+
+/* Bytes of workspace bc_packed_decode_ws needs for this shape. */
+size_t bc_packed_decode_workspace_size(bc_shape shape);
+
+/* bc_packed_decode with long sequences split into fixed token chunks across
+ * workgroups and an FP32 merge; chunking depends on shape.max_pages only,
+ * so no device lengths are read on the host.  A null or undersized
+ * workspace falls back to bc_packed_decode. */
+int bc_packed_decode_ws(bc_shape shape, const bc_half* q,
+                        const bc_half* packed_kv, const int32_t* pages,
+                        const int32_t* lengths, bc_half* output,
+                        long long block_stride, long long head_stride,
+                        long long slot_stride, long long kv_stride,
+                        float scale, void* workspace, size_t workspace_bytes,
+                        bc_stream_t stream);
+
+/* Library version string, for logs. */
+const char* bc_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* BRANCHCRAFT_H_ */

@@ -1,0 +1,144 @@
+"""Calls into libbranchcraft_hip.so through the C ABI with torch-owned
+device memory (torch is only the allocator and stream provider here)."""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import torch
+
+import branchcraft_capi as capi
+
+PAGE = 16
+
+
+def lib():
+    return capi.load()
+
+
+def stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def dev(a, dtype=None) -> torch.Tensor:
+    t = torch.from_numpy(np.ascontiguousarray(a))
+    if dtype is not None:
+        t = t.to(dtype)
+    return t.to("cuda")
+
+
+def check(err: int, what: str) -> None:
+    assert err == capi.BC_SUCCESS, f"{what} returned {err}"
+
+
+def decode(q, k, v, pages, lengths, splits, *, keep=False, out=None):
+    """bc_decode on numpy inputs; returns the FP32 output as numpy."""
+    b, hq, d = q.shape
+    P, _, hkv, _ = k.shape
+    tq, tk, tv = dev(q), dev(k), dev(v)
+    tp, tl = dev(pages.astype(np.int32)), dev(lengths.astype(np.int32))
+    o = torch.full((b, hq, d), float("nan"), device="cuda", dtype=torch.float32)
+    pa = torch.empty(max(1, splits * b * hq * d), device="cuda", dtype=torch.float32)
+    pml = torch.empty(max(1, splits * b * hq * 2), device="cuda", dtype=torch.float32)
+    shape = capi.Shape(b, hq, hkv, d, pages.shape[1], P)
+    ins = capi.Inputs(tq.data_ptr(), tk.data_ptr(), tv.data_ptr(), tp.data_ptr(),
+                      tl.data_ptr(), o.data_ptr())
+    scr = capi.Scratch(pa.data_ptr(), pml.data_ptr())
+    check(lib().bc_decode(shape, ins, scr, splits, stream()), "bc_decode")
+    torch.cuda.synchronize()
+    return o.cpu().numpy()
+
+
+def tree(k, v, pages, lengths, dq, dk, dv, parent, *, workspace=True):
+    b, n, hq, d = dq.shape
+    P, _, hkv, _ = k.shape
+    tk, tv = dev(k), dev(v)
+    tp, tl = dev(pages.astype(np.int32)), dev(lengths.astype(np.int32))
+    tq, tdk, tdv = dev(dq), dev(dk), dev(dv)
+    tpar = dev(parent.astype(np.int32))
+    o = torch.full((b, n, hq, d), float("nan"), device="cuda", dtype=torch.float32)
+    shape = capi.Shape(b, hq, hkv, d, pages.shape[1], P)
+    prefix = capi.Inputs(None, tk.data_ptr(), tv.data_ptr(), tp.data_ptr(), tl.data_ptr(),
+                         None)
+    ins = capi.TreeInputs(prefix, tq.data_ptr(), tdk.data_ptr(), tdv.data_ptr(),
+                          tpar.data_ptr(), o.data_ptr())
+    L = lib()
+    if workspace:
+        nbytes = L.bc_tree_verify_workspace_size(shape, n)
+        ws = torch.empty(max(1, nbytes), device="cuda", dtype=torch.uint8)
+        check(L.bc_tree_verify_ws(shape, ins, n, ws.data_ptr(), nbytes, stream()),
+              "bc_tree_verify_ws")
+    else:
+        check(L.bc_tree_verify(shape, ins, n, stream()), "bc_tree_verify")
+    torch.cuda.synchronize()
+    return o.cpu().numpy()
+
+
+def packed(q, cache: torch.Tensor, strides, hkv, phys_pages, pages, lengths, scale, *,
+           workspace=True):
+    """cache: a GPU FP16 tensor whose storage holds the packed pool; strides
+    are element strides relative to cache.data_ptr()."""
+    b, hq, d = q.shape
+    tq = dev(q)
+    tp, tl = dev(pages.astype(np.int32)), dev(lengths.astype(np.int32))
+    o = torch.full((b, hq, d), float("nan"), device="cuda", dtype=torch.float16)
+    shape = capi.Shape(b, hq, hkv, d, pages.shape[1], phys_pages)
+    bs, hs, ss, kvs = (int(x) for x in strides)
+    L = lib()
+    if workspace:
+        nbytes = L.bc_packed_decode_workspace_size(shape)
+        ws = torch.empty(max(1, nbytes), device="cuda", dtype=torch.uint8)
+        check(L.bc_packed_decode_ws(shape, tq.data_ptr(), cache.data_ptr(), tp.data_ptr(),
+                                    tl.data_ptr(), o.data_ptr(), bs, hs, ss, kvs,
+                                    float(scale), ws.data_ptr(), nbytes, stream()),
+              "bc_packed_decode_ws")
+    else:
+        check(L.bc_packed_decode(shape, tq.data_ptr(), cache.data_ptr(), tp.data_ptr(),
+                                 tl.data_ptr(), o.data_ptr(), bs, hs, ss, kvs,
+                                 float(scale), stream()), "bc_packed_decode")
+    torch.cuda.synchronize()
+    return o.cpu().numpy()
+
+
+def commit(cache_k: torch.Tensor, cache_v: torch.Tensor, dk: torch.Tensor,
+           dv: torch.Tensor, path, dest_pages, dest_slots, request: int):
+    b, n, hkv, d = dk.shape
+    tpath = torch.tensor(path, device="cuda", dtype=torch.int32)
+    tdp = torch.tensor(dest_pages, device="cuda", dtype=torch.int32)
+    tds = torch.tensor(dest_slots, device="cuda", dtype=torch.int32)
+    shape = capi.Shape(b, hkv, hkv, d, 1, cache_k.shape[0])
+    check(lib().bc_commit_path(shape, dk.data_ptr(), dv.data_ptr(), cache_k.data_ptr(),
+                               cache_v.data_ptr(), tpath.data_ptr(), tdp.data_ptr(),
+                               tds.data_ptr(), request, n, len(path), stream()),
+          "bc_commit_path")
+    torch.cuda.synchronize()
+
+
+def copy_pages(cache_k: torch.Tensor, cache_v: torch.Tensor, src, dst):
+    _, _, hkv, d = cache_k.shape
+    ts = torch.tensor(src, device="cuda", dtype=torch.int32)
+    td = torch.tensor(dst, device="cuda", dtype=torch.int32)
+    shape = capi.Shape(1, hkv, hkv, d, 1, cache_k.shape[0])
+    check(lib().bc_copy_pages(shape, cache_k.data_ptr(), cache_v.data_ptr(), ts.data_ptr(),
+                              td.data_ptr(), len(src), stream()), "bc_copy_pages")
+    torch.cuda.synchronize()
+
+
+def f16_tolerance(expected: np.ndarray, atol: float) -> np.ndarray:
+    """Allowed |fp16 result - fp32 oracle|: the kernel tolerance plus half an
+    FP16 ulp of the expected value (round-to-nearest of the output)."""
+    ulp = np.spacing(np.abs(expected).astype(np.float16)).astype(np.float32)
+    return atol + 0.5 * ulp
+
+
+def gate(actual, expected, atol, what):
+    err = float(np.max(np.abs(actual.astype(np.float64) - expected.astype(np.float64)))) \
+        if actual.size else 0.0
+    assert np.all(np.isfinite(actual)), f"{what}: non-finite output"
+    assert err <= atol, f"{what}: max abs error {err:.3e} > {atol:.1e}"
+    return err
+
+
+def rsqrt(d):
+    return 1.0 / math.sqrt(d)

@@ -1,0 +1,88 @@
+"""Paged GQA decode (bc_decode) against the CPU oracle.
+
+Cases restate the reference driver's suite (src/main.cu:318-352): empty,
+single token, page boundary 16/17, ragged batch, non-power-of-two GQA
+(10/2, 12/3), D=64/128 and splits 1..16 at its 3e-4 gate; then splits
+beyond the reference's cap, BASELINE config 1 and config 4 at full size.
+"""
+
+import numpy as np
+import pytest
+
+from oracle import oracle_np
+import gpu_helpers as G
+
+pytestmark = pytest.mark.gpu
+
+REF_CASES = [
+    (1, 8, 2, 64, [0]), (1, 8, 2, 64, [1]), (1, 8, 2, 64, [16]), (1, 8, 2, 64, [17]),
+    (3, 10, 2, 64, [0, 37, 91]), (3, 12, 3, 128, [7, 128, 257]), (2, 32, 8, 128, [513, 3]),
+]
+
+
+@pytest.mark.parametrize("case", REF_CASES, ids=lambda c: f"B{c[0]}_H{c[1]}x{c[2]}_D{c[3]}")
+def test_reference_cases_all_splits(case, oracle):
+    b, hq, hkv, d, lens = case
+    rng = np.random.default_rng(17)
+    q, k, v, pages, lengths = oracle_np.paged_fixture(rng, b, hq, hkv, d, lens)
+    expected = oracle.decode(q, k, v, pages, lengths)
+    for splits in (1, 2, 4, 8, 16, 33, 64):
+        out = G.decode(q, k, v, pages, lengths, splits)
+        G.gate(out, expected, 3e-4, f"splits={splits}")
+
+
+def test_config1_b1_l512(oracle):
+    """B=1, L=512, 32/8 heads, D=128, pool of 64 pages,
+    page table = first 32 ids of a seeded permutation, N(0,1)."""
+    rng = np.random.default_rng(1)
+    perm = rng.permutation(64).astype(np.int32)
+    pages = perm[:32].reshape(1, 32)
+    lengths = np.array([512], dtype=np.int32)
+    q = rng.standard_normal((1, 32, 128)).astype(np.float16)
+    k = rng.standard_normal((64, 16, 8, 128)).astype(np.float16)
+    v = rng.standard_normal((64, 16, 8, 128)).astype(np.float16)
+    expected = oracle.decode(q, k, v, pages, lengths)
+    closed = oracle_np.decode(q, k, v, pages, lengths)
+    G.gate(expected, closed, 1e-5, "oracle vs float64 closed form")
+    for splits in (1, 2, 4, 8):
+        G.gate(G.decode(q, k, v, pages, lengths, splits), expected, 3e-4, f"splits={splits}")
+
+
+def test_config4_split_k_long_context(oracle):
+    """B=4, L ~ U[16384, 32768], random page map; the
+    split count keeps chunks in [256, 2048] tokens."""
+    rng = np.random.default_rng(4)
+    lens = rng.integers(16384, 32769, size=4)
+    q, k, v, pages, lengths = oracle_np.paged_fixture(rng, 4, 32, 8, 128, lens, spare=16,
+                                                     sigma=1.0)
+    expected = oracle.decode(q, k, v, pages, lengths, threads=16)
+    for splits in (16, 64):
+        out = G.decode(q, k, v, pages, lengths, splits)
+        G.gate(out, expected, 2e-3, f"config4 splits={splits}")
+        G.gate(out, expected, 3e-4, f"config4 splits={splits} (reference gate)")
+
+
+def test_garbage_in_unused_slots_is_ignored(oracle):
+    """Slots past a sequence's length (in its last page) may hold NaN/inf;
+    they must not reach the output."""
+    rng = np.random.default_rng(5)
+    q, k, v, pages, lengths = oracle_np.paged_fixture(rng, 3, 8, 2, 128, [5, 33, 16])
+    expected = oracle.decode(q, k, v, pages, lengths)
+    k2, v2 = k.copy(), v.copy()
+    for bi, n in enumerate(lengths):
+        if n % 16:
+            last = pages[bi, n // 16]
+            k2[last, n % 16:] = np.float16(np.nan)
+            v2[last, n % 16:] = np.float16(np.inf)
+    for splits in (1, 3):
+        G.gate(G.decode(q, k2, v2, pages, lengths, splits), expected, 3e-4, "garbage slots")
+
+
+def test_split_matches_single_at_scale():
+    """Split-K and single-partition results agree (src/main.cu:505-509)."""
+    rng = np.random.default_rng(9)
+    lens = [8192 - (i % 4) * 1024 for i in range(8)]
+    q, k, v, pages, lengths = oracle_np.paged_fixture(rng, 8, 32, 8, 128, lens)
+    single = G.decode(q, k, v, pages, lengths, 1)
+    for splits in (2, 16, 128):
+        G.gate(G.decode(q, k, v, pages, lengths, splits), single, 3e-4, f"splits={splits}")

@@ -1,0 +1,114 @@
+"""Packed-cache decode (bc_packed_decode[_ws]) against the CPU oracle.
+
+Restates the reference's packed test (tests/test_torch_ops.py:62-96: HND and
+NHD strides, lengths [23, 9, 0]) and adds the [P,2,16,Hkv,D] layout of
+BASELINE config 5, unaligned strides, the split/unsplit paths and config 5
+at full size.  FP16 outputs are gated at 2e-3 plus half an FP16 ulp.
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle_np
+import gpu_helpers as G
+
+pytestmark = pytest.mark.gpu
+
+
+def _run_both(q, cache, strides, hkv, phys, pages, lengths, scale, oracle, atol=2e-3):
+    exp32, _ = oracle.packed_decode(q, cache.cpu().numpy(), pages, lengths, strides, hkv,
+                                    scale)
+    for ws in (False, True):
+        out = G.packed(q, cache, strides, hkv, phys, pages, lengths, scale, workspace=ws)
+        tol = G.f16_tolerance(exp32, atol)
+        err = np.abs(out.astype(np.float32) - exp32)
+        assert np.all(np.isfinite(out)), "non-finite output"
+        assert np.all(err <= tol), f"workspace={ws}: max err {err.max():.3e}"
+    return exp32
+
+
+@pytest.mark.parametrize("layout", ["HND", "NHD"])
+@pytest.mark.parametrize("dim", [64, 128])
+def test_reference_packed_layouts(layout, dim, oracle):
+    rng = np.random.default_rng(11)
+    batch, hq, hkv = 3, 8, 2
+    if layout == "HND":
+        base = torch.from_numpy(rng.standard_normal((9, hkv, 16, 2 * dim)).astype(np.float16))
+        cache = base.cuda()
+        strides = (cache.stride(0), cache.stride(1), cache.stride(2), dim)
+    else:
+        base = torch.from_numpy(rng.standard_normal((9, 16, hkv, 2 * dim)).astype(np.float16))
+        cache = base.cuda()  # physical NHD; logical HND view = transpose(1, 2)
+        view = cache.transpose(1, 2)
+        strides = (view.stride(0), view.stride(1), view.stride(2), dim)
+    q = rng.standard_normal((batch, hq, dim)).astype(np.float16)
+    pages = np.array([[4, 1], [2, 7], [8, 6]], dtype=np.int32)
+    lengths = np.array([23, 9, 0], dtype=np.int32)
+    exp32 = _run_both(q, cache, strides, hkv, 9, pages, lengths, 1 / math.sqrt(dim), oracle)
+    # Closed-form pin of the oracle on the same inputs.
+    closed = oracle_np.packed_decode(q, cache.cpu().numpy().reshape(-1), strides, hkv, 9,
+                                     pages, lengths, 1 / math.sqrt(dim))
+    G.gate(exp32, closed, 1e-5, "oracle vs closed form")
+    assert np.all(exp32[2] == 0), "empty sequence must give zeros"
+
+
+def test_five_dim_layout_small(oracle):
+    """[P, 2, 16, Hkv, D]: K at block*16*2*Hkv*D + slot*Hkv*D + head*D, V at
+    +16*Hkv*D (BASELINE config 5's layout) at a small size."""
+    rng = np.random.default_rng(3)
+    P, hkv, d, hq, b = 40, 8, 128, 32, 5
+    cache = torch.from_numpy(rng.standard_normal((P, 2, 16, hkv, d)).astype(np.float16)).cuda()
+    strides = (cache.stride(0), cache.stride(3), cache.stride(2), cache.stride(1))
+    lengths = np.array([1, 16, 17, 200, 0], dtype=np.int32)
+    perm = rng.permutation(P).astype(np.int32)
+    pages = np.full((b, 13), -1, dtype=np.int32)
+    cur = 0
+    for i, n in enumerate(lengths):
+        c = -(-int(n) // 16)
+        pages[i, :c] = perm[cur:cur + c]
+        cur += c
+    q = rng.standard_normal((b, hq, d)).astype(np.float16)
+    _run_both(q, cache, strides, hkv, P, pages, lengths, 0.07, oracle)
+
+
+def test_unaligned_strides_take_the_scalar_path(oracle):
+    """Strides that are not multiples of 8 elements still decode correctly."""
+    rng = np.random.default_rng(13)
+    P, hkv, d, hq, b = 6, 2, 64, 4, 2
+    ss, hs = 2 * d + 1, 16 * (2 * d + 1) + 3
+    bs = hkv * hs + 5
+    flat = torch.from_numpy(rng.standard_normal(P * bs + 16).astype(np.float16)).cuda()
+    strides = (bs, hs, ss, d)
+    pages = np.array([[3, 0], [5, 1]], dtype=np.int32)
+    lengths = np.array([20, 31], dtype=np.int32)
+    q = rng.standard_normal((b, hq, d)).astype(np.float16)
+    _run_both(q, flat, strides, hkv, P, pages, lengths, 0.125, oracle)
+
+
+def test_config5_full_size(oracle):
+    """B=64, contexts U[128, 4096], cache [20000,2,16,8,128],
+    block-table rows = consecutive slices of a seeded permutation."""
+    rng = np.random.default_rng(5)
+    B, hq, hkv, d, NB, maxp = 64, 32, 8, 128, 20000, 256
+    g = torch.Generator(device="cuda").manual_seed(5)
+    cache = torch.randn((NB, 2, 16, hkv, d), generator=g, device="cuda", dtype=torch.float16)
+    lengths = rng.integers(128, 4097, size=B).astype(np.int32)
+    perm = rng.permutation(NB).astype(np.int32)
+    pages = np.full((B, maxp), -1, dtype=np.int32)
+    cur = 0
+    for i, n in enumerate(lengths):
+        c = -(-int(n) // 16)
+        pages[i, :c] = perm[cur:cur + c]
+        cur += c
+    q = rng.standard_normal((B, hq, d)).astype(np.float16)
+    strides = (cache.stride(0), cache.stride(3), cache.stride(2), cache.stride(1))
+    scale = 1 / math.sqrt(d)
+    exp32, _ = oracle.packed_decode(q, cache.cpu().numpy(), pages, lengths, strides, hkv,
+                                    scale, threads=16)
+    for ws in (True, False):
+        out = G.packed(q, cache, strides, hkv, NB, pages, lengths, scale, workspace=ws)
+        err = np.abs(out.astype(np.float32) - exp32)
+        assert np.all(err <= G.f16_tolerance(exp32, 2e-3)), f"ws={ws} max err {err.max():.3e}"

@@ -1,0 +1,93 @@
+"""Tree verification (bc_tree_verify[_ws]) against the CPU oracle.
+
+Restates the reference driver's tree cases (src/main.cu:252-262: prefix
+{0, 17, 257}, B=2, N=7, binary parents, 3e-4), the reference torch test
+(tests/test_torch_ops.py:16-53), BASELINE configs 2 and 3, deep/wide trees
+over several MFMA row and draft tiles, and the invariant that the tree
+output equals paged decode over the expanded-prefix fixture
+(src/main.cu:375-423, 457-463).
+"""
+
+import numpy as np
+import pytest
+
+from oracle import oracle_np
+import gpu_helpers as G
+
+pytestmark = pytest.mark.gpu
+
+
+def _check(fix, oracle, atol=3e-4, what=""):
+    k, v, pages, lengths, dq, dk, dv, par = fix
+    expected = oracle.tree(k, v, pages, lengths, dq, dk, dv, par, threads=16)
+    for ws in (False, True):
+        out = G.tree(k, v, pages, lengths, dq, dk, dv, par, workspace=ws)
+        G.gate(out, expected, atol, f"{what} workspace={ws}")
+    return expected
+
+
+@pytest.mark.parametrize("prefix,dim", [(0, 64), (17, 64), (257, 128)])
+def test_reference_tree_cases(prefix, dim, oracle):
+    rng = np.random.default_rng(31)
+    fix = oracle_np.tree_fixture(rng, 2, prefix, 7, d=dim)
+    _check(fix, oracle, what=f"prefix={prefix}")
+
+
+@pytest.mark.parametrize("dim", [64, 128])
+def test_reference_torch_tree_case(dim, oracle):
+    rng = np.random.default_rng(7)
+    batch, nodes, hq, hkv = 2, 7, 4, 2
+    dq = rng.standard_normal((batch, nodes, hq, dim)).astype(np.float16)
+    k = rng.standard_normal((7, 16, hkv, dim)).astype(np.float16)
+    v = rng.standard_normal((7, 16, hkv, dim)).astype(np.float16)
+    pages = np.array([[4, 1], [5, 2]], dtype=np.int32)
+    lengths = np.array([23, 0], dtype=np.int32)
+    dk = rng.standard_normal((batch, nodes, hkv, dim)).astype(np.float16)
+    dv = rng.standard_normal((batch, nodes, hkv, dim)).astype(np.float16)
+    par = np.array([[-1, 0, 0, 1, 1, 2, 2]] * batch, dtype=np.int32)
+    exp = _check((k, v, pages, lengths, dq, dk, dv, par), oracle, atol=3e-4)
+    closed = oracle_np.tree(k, v, pages, lengths, dq, dk, dv, par)
+    G.gate(exp, closed, 1e-5, "oracle vs closed form")
+
+
+def test_config2_single_request_2048(oracle):
+    rng = np.random.default_rng(2)
+    fix = oracle_np.tree_fixture(rng, 1, 2048, 7, sigma=1.0, parents="random")
+    _check(fix, oracle, atol=3e-4, what="config2")
+
+
+def test_config3_eight_requests_shared_partial_prefix(oracle):
+    rng = np.random.default_rng(3)
+    fix = oracle_np.tree_fixture(rng, 8, 2053, 7, sigma=1.0, parents="random")
+    _check(fix, oracle, atol=3e-4, what="config3")
+
+
+@pytest.mark.parametrize("nodes,hq,hkv", [(40, 32, 8), (256, 8, 8), (33, 4, 2)])
+def test_wide_trees_span_row_and_draft_tiles(nodes, hq, hkv, oracle):
+    rng = np.random.default_rng(nodes)
+    fix = oracle_np.tree_fixture(rng, 2, 70, nodes, hq=hq, hkv=hkv, d=128,
+                                 parents="random")
+    _check(fix, oracle, atol=3e-4, what=f"N={nodes}")
+
+
+def test_tree_equals_expanded_decode(oracle):
+    rng = np.random.default_rng(91)
+    k, v, pages, lengths, dq, dk, dv, par = oracle_np.tree_fixture(rng, 4, 300, 7,
+                                                                   parents="random")
+    tree = G.tree(k, v, pages, lengths, dq, dk, dv, par)
+    el, ep, ek, ev = oracle.expand_tree(k, v, pages, lengths, dk, dv, par)
+    b, n, hq, d = dq.shape
+    flat = G.decode(dq.reshape(b * n, hq, d), ek, ev, ep, el, 1)
+    G.gate(flat.reshape(tree.shape), tree, 3e-4, "tree vs expanded decode")
+
+
+def test_garbage_past_prefix_is_ignored(oracle):
+    rng = np.random.default_rng(12)
+    k, v, pages, lengths, dq, dk, dv, par = oracle_np.tree_fixture(rng, 2, 37, 7)
+    expected = oracle.tree(k, v, pages, lengths, dq, dk, dv, par)
+    last = pages[0, 37 // 16]
+    k[last, 37 % 16:] = np.float16(np.nan)
+    v[last, 37 % 16:] = np.float16(np.inf)
+    for ws in (False, True):
+        G.gate(G.tree(k, v, pages, lengths, dq, dk, dv, par, workspace=ws), expected, 3e-4,
+               "garbage slots")
