@@ -181,6 +181,9 @@ __global__ __launch_bounds__(kThreads) void paged_attn_kernel(AttnParams P) {
           const bool ok = valid_c && t >= begin && t < end;
 #pragma unroll
           for (int hh = 0; hh < HB; ++hh) s[i][hh] = ok ? s[i][hh] : kNegInf;
+          // Slots past the length may hold any bits (NaN included); their
+          // weight is zero, so their V row must be zero too.
+          if (!ok) vc[i] = make_uint4(0, 0, 0, 0);
         }
       }
 

@@ -10,6 +10,9 @@
 //   S^T[32 tok x 32 rows] = K[32 tok x D] . Q^T[D x 32 rows]   (D/16 MFMAs)
 //   O^T[D x 32 rows]     += V^T[D x 32 tok] . P^T[32 tok x 32 rows]
 //
+// P enters the second product as an FP16 hi/lo pair (two MFMAs), so the
+// only rounding left is the FP32 accumulation.
+//
 // K tiles feed the A operand straight from HBM (16 contiguous bytes per lane
 // per MFMA).  The S^T accumulator layout is, lane for lane, the B operand of
 // the P.V product once the token order inside a 16-token step is permuted
@@ -244,13 +247,17 @@ __global__ __launch_bounds__(kThreads) void tree_kernel(TreeParams P) {
         for (int j = 0; j < 16; ++j) acc[dt][j] *= alpha;
       m = mnew;
     }
+    // P is split into FP16 hi + lo parts (two MFMAs each) so the P.V product
+    // carries ~22 bits of P instead of FP16's 11.
     const float mb = safe_max(m);
-    f16x8 pb[2];
+    f16x8 pb[2], pl[2];
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
       const float pr = fast_exp2(sv[j] - mb);
       l += pr;
-      pb[j >> 3][j & 7] = (_Float16)pr;
+      const _Float16 hi = (_Float16)pr;
+      pb[j >> 3][j & 7] = hi;
+      pl[j >> 3][j & 7] = (_Float16)(pr - (float)hi);
     }
 
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -265,6 +272,7 @@ __global__ __launch_bounds__(kThreads) void tree_kernel(TreeParams P) {
         const f16x4 hi = lds_read_tr(vtr + (16 * st + 8) * VP + 32 * dt);
         const f16x8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
         acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pb[st], acc[dt], 0, 0, 0);
+        acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pl[st], acc[dt], 0, 0, 0);
       }
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");

@@ -252,8 +252,13 @@ static void tree_row(const void* vctx, int row, void* scratch) {
     vp[count] = c->v + off;
     ++count;
   }
+  /* ancestor chain; a node is visited once (a cyclic parent array ends at
+     the first repeat) */
   int cur = node;
-  for (int steps = 0; steps < N && cur >= 0 && cur < N; ++steps) {
+  unsigned char* seen = (unsigned char*)(scores + len + N);
+  memset(seen, 0, (size_t)N);
+  while (cur >= 0 && cur < N && !seen[cur]) {
+    seen[cur] = 1;
     const size_t off = (((size_t)b * N + cur) * c->hkv + kvh) * D;
     kp[count] = c->dk + off;
     vp[count] = c->dv + off;
@@ -304,7 +309,7 @@ void oracle_tree(int batch, int nodes, int hq, int hkv, int dim, int max_pages,
   c.out = out;
   const size_t tokens = (size_t)max_pages * ORACLE_PAGE + nodes;
   run_rows(tree_row, &c, batch * nodes * hq, threads,
-           tokens * (2 * sizeof(void*) + sizeof(double)) + 64);
+           tokens * (2 * sizeof(void*) + sizeof(double)) + (size_t)nodes + 64);
 }
 
 /* ---- bit copies ------------------------------------------------------- */
@@ -344,7 +349,10 @@ void oracle_copy_pages(int hkv, int dim, int phys_pages, uint16_t* cache_k,
 
 static int chain(const int32_t* parent_row, int nodes, int node, int* path) {
   int n = 0, cur = node;
-  while (n < nodes && cur >= 0 && cur < nodes) {
+  while (cur >= 0 && cur < nodes) {
+    int repeat = 0;
+    for (int i = 0; i < n; ++i) repeat |= path[i] == cur;
+    if (repeat) break;
     path[n++] = cur;
     cur = parent_row[cur];
   }

@@ -55,7 +55,7 @@ void oracle_packed_decode(int batch, int hq, int hkv, int dim, int max_pages,
  * every node attends to its request's prefix plus its ancestor chain
  * (itself included), all in double.  draft_q [B,N,Hq,D]; draft_k/v
  * [B,N,Hkv,D]; parent [B,N]; out [B,N,Hq,D] f32.  The parent walk stops at
- * a parent outside [0, N) or after N steps. */
+ * a parent outside [0, N) or at a node it already visited. */
 void oracle_tree(int batch, int nodes, int hq, int hkv, int dim, int max_pages,
                  const uint16_t* k, const uint16_t* v, const int32_t* pages,
                  const int32_t* lengths, const uint16_t* draft_q,

@@ -71,11 +71,12 @@ def packed_decode(q, cache_flat, strides, hkv, phys_pages, pages, lengths, scale
 
 
 def ancestors(parent_row, node):
-    """Brute force: the set reached from node by following parents, bounded."""
+    """Brute force: the nodes reached from node by following parents, each
+    once; the walk ends at a parent outside [0, N) or at a repeated node."""
     n = len(parent_row)
     seen = []
     cur = node
-    while 0 <= cur < n and len(seen) < n:
+    while 0 <= cur < n and cur not in seen:
         seen.append(cur)
         cur = int(parent_row[cur])
     return seen
