@@ -69,6 +69,23 @@ __device__ __forceinline__ float group_sum(float x) {
   return x;
 }
 
+// group_sum over N independent values, one DPP step at a time across all of
+// them, so consecutive DPP reads never depend on the instruction just before.
+template <int GROUP, int N>
+__device__ __forceinline__ void group_sum_n(float (&x)[N]) {
+  static_assert(GROUP == 8 || GROUP == 16, "group of 8 or 16 lanes");
+  if (GROUP == 16) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) x[i] += dpp_f<kDppRowMirror>(x[i]);
+  }
+#pragma unroll
+  for (int i = 0; i < N; ++i) x[i] += dpp_f<kDppRowHalfMirror>(x[i]);
+#pragma unroll
+  for (int i = 0; i < N; ++i) x[i] += dpp_f<kDppQuadXor2>(x[i]);
+#pragma unroll
+  for (int i = 0; i < N; ++i) x[i] += dpp_f<kDppQuadXor1>(x[i]);
+}
+
 template <int GROUP>
 __device__ __forceinline__ float group_max(float x) {
   static_assert(GROUP == 8 || GROUP == 16, "group of 8 or 16 lanes");

@@ -359,29 +359,47 @@ __global__ __launch_bounds__(kThreads) void tree_kernel(TreeParams P) {
   }
 }
 
-// Combines the prefix chunks and the draft part of every (b, node, h).
+// Combines the prefix chunks and the draft part of every (b, node, h): one
+// wave per output row, lane p reads slot p's (max, sum), the weights are
+// formed once and every lane accumulates its dims with independent loads.
 template <int D>
 __global__ __launch_bounds__(256) void merge_tree_kernel(TreeParams P) {
-  const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
-  const size_t total = (size_t)P.batch * P.nodes * P.hq * D;
-  if (idx >= total) return;
-  const int d = idx % D;
-  const size_t row = idx / D;  // (b*N + node)*Hq + h
+  constexpr int PER = D / 64;
+  const int lane = threadIdx.x & 63;
+  const size_t row = (size_t)blockIdx.x * 4 + (threadIdx.x >> 6);  // (b*N+node)*Hq+h
+  if (row >= (size_t)P.batch * P.nodes * P.hq) return;
   const int b = row / ((size_t)P.nodes * P.hq);
   const int len = max(0, min(P.lengths[b], P.max_pages * BC_PAGE_SIZE));
   const int nparts = (len + P.chunk_tokens - 1) / P.chunk_tokens;
   if (nparts == 0) return;  // the draft part wrote the final output
   const size_t base = row * (P.prefix_parts + 1);
-  float mm = P.part_ml[2 * (base + P.prefix_parts)];
-  for (int p = 0; p < nparts; ++p) mm = __builtin_fmaxf(mm, P.part_ml[2 * (base + p)]);
-  float lsum = 0.f, asum = 0.f;
-  for (int p = 0; p <= nparts; ++p) {
-    const size_t s = base + (p == nparts ? P.prefix_parts : p);
-    const float w = fast_exp2(P.part_ml[2 * s] - mm);
-    lsum += w * P.part_ml[2 * s + 1];
-    asum += w * P.part_acc[s * D + d];
+  // slot of part i: prefix chunks 0..nparts-1, then the draft slot
+  auto slot = [&](int i) { return base + (i == nparts ? P.prefix_parts : i); };
+  float mp = kNegInf, lp = 0.f;
+  if (lane <= nparts) {  // nparts < 64 is guaranteed by tree_chunking
+    mp = P.part_ml[2 * slot(lane)];
+    lp = P.part_ml[2 * slot(lane) + 1];
   }
-  P.out[idx] = asum / lsum;
+  float mm = mp;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) mm = __builtin_fmaxf(mm, shfl_xor_f(mm, off));
+  const float w = fast_exp2(mp - mm);  // every row sees its own node: mm finite
+  float lsum = w * lp;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) lsum += shfl_xor_f(lsum, off);
+  float a[PER];
+#pragma unroll
+  for (int j = 0; j < PER; ++j) a[j] = 0.f;
+  for (int i = 0; i <= nparts; ++i) {
+    const float wi = __builtin_bit_cast(float, __builtin_amdgcn_readlane(
+                                                   __builtin_bit_cast(int, w), i));
+    const float* src = P.part_acc + slot(i) * D + lane;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) a[j] += wi * src[64 * j];
+  }
+  const float inv = 1.f / lsum;
+#pragma unroll
+  for (int j = 0; j < PER; ++j) P.out[row * D + lane + 64 * j] = a[j] * inv;
 }
 
 bool tree_args_ok(const bc_shape& s, const bc_tree_inputs& in, int nodes) {
@@ -434,6 +452,9 @@ void tree_chunking(const bc_shape& s, int nodes, int* chunk_tokens, int* parts) 
   int chunk = (int)((max_tokens + want - 1) / want);
   chunk = (chunk + kTile - 1) / kTile * kTile;
   if (chunk < 128) chunk = 128;
+  // The merge reads one partial per lane: at most 63 prefix chunks.
+  const int min_chunk = (max_tokens + 62) / 63;
+  if (chunk < min_chunk) chunk = (min_chunk + kTile - 1) / kTile * kTile;
   *chunk_tokens = chunk;
   *parts = (max_tokens + chunk - 1) / chunk;
 }
@@ -452,8 +473,8 @@ hipError_t launch_tree(TreeParams& P, int dim, int parts, hipStream_t st) {
   else tree_kernel<128><<<grid, kThreads, 0, st>>>(P);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess || !P.part_acc) return err;
-  const size_t n = (size_t)P.batch * P.nodes * P.hq * dim;
-  const dim3 mgrid((unsigned)((n + 255) / 256));
+  const size_t rows = (size_t)P.batch * P.nodes * P.hq;
+  const dim3 mgrid((unsigned)((rows + 3) / 4));
   if (dim == 64) merge_tree_kernel<64><<<mgrid, 256, 0, st>>>(P);
   else merge_tree_kernel<128><<<mgrid, 256, 0, st>>>(P);
   return hipGetLastError();

@@ -1,0 +1,193 @@
+"""The C ABI loads without a GPU, exports every declared entry point and
+rejects bad arguments with hipErrorInvalidValue before touching the device.
+
+Rejection rules restate the reference's checks: src/paged_gqa.cu:124-129,
+src/tree_attention.cu:94-99 and 111-114, src/packed_decode.cu:69-73 and the
+driver's API test (src/main.cu:343-349).  No call here reaches a launch.
+"""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+import branchcraft_capi as capi
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "branchcraft.h"
+INVALID = capi.BC_ERROR_INVALID_VALUE
+FAKE = 0x1000  # a non-null address; never dereferenced on the rejection path
+
+
+def declared_symbols():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"\b(bc_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = capi.load()
+    names = declared_symbols()
+    assert len(names) >= 11
+    for name in names:
+        assert hasattr(lib, name), f"{name} missing from {capi.LIB_PATH}"
+    assert set(names) == set(capi.EXPORTED)
+    assert b"gfx950" in lib.bc_version()
+
+
+def _shape(**kw):
+    base = dict(batch=2, query_heads=32, kv_heads=8, dim=128, max_pages=4, physical_pages=16)
+    base.update(kw)
+    return capi.Shape(**base)
+
+
+def _inputs(**kw):
+    base = dict(q=FAKE, k=FAKE, v=FAKE, pages=FAKE, lengths=FAKE, output=FAKE)
+    base.update(kw)
+    return capi.Inputs(**base)
+
+
+BAD_DECODE = [
+    ("dim96", dict(shape=dict(dim=96))),
+    ("batch0", dict(shape=dict(batch=0))),
+    ("hq_not_multiple", dict(shape=dict(query_heads=30))),
+    ("kv0", dict(shape=dict(kv_heads=0))),
+    ("max_pages0", dict(shape=dict(max_pages=0))),
+    ("phys0", dict(shape=dict(physical_pages=0))),
+    ("splits0", dict(splits=0)),
+    ("splits_over_cap", dict(splits=capi.BC_MAX_SPLITS + 1)),
+    ("null_q", dict(inputs=dict(q=None))),
+    ("null_pages", dict(inputs=dict(pages=None))),
+    ("null_out", dict(inputs=dict(output=None))),
+    ("null_scratch_split2", dict(splits=2, scratch=(None, None))),
+    ("half_scratch_split2", dict(splits=2, scratch=(FAKE, None))),
+]
+
+
+@pytest.mark.parametrize("name,case", BAD_DECODE, ids=[c[0] for c in BAD_DECODE])
+def test_decode_rejects(name, case):
+    lib = capi.load()
+    shape = _shape(**case.get("shape", {}))
+    ins = _inputs(**case.get("inputs", {}))
+    scr = capi.Scratch(*case.get("scratch", (FAKE, FAKE)))
+    assert lib.bc_decode(shape, ins, scr, case.get("splits", 1), None) == INVALID
+
+
+def _tree_inputs(**kw):
+    prefix = capi.Inputs(None, FAKE, FAKE, FAKE, FAKE, None)
+    base = dict(draft_q=FAKE, draft_k=FAKE, draft_v=FAKE, parent=FAKE, output=FAKE)
+    base.update(kw)
+    return capi.TreeInputs(prefix, **base)
+
+
+@pytest.mark.parametrize("nodes", [0, capi.BC_MAX_TREE_NODES + 1])
+def test_tree_rejects_node_count(nodes):
+    lib = capi.load()
+    assert lib.bc_tree_verify(_shape(), _tree_inputs(), nodes, None) == INVALID
+    assert lib.bc_tree_verify_ws(_shape(), _tree_inputs(), nodes, None, 0, None) == INVALID
+
+
+@pytest.mark.parametrize("field", ["draft_q", "draft_k", "draft_v", "parent", "output"])
+def test_tree_rejects_null(field):
+    lib = capi.load()
+    assert lib.bc_tree_verify(_shape(), _tree_inputs(**{field: None}), 7, None) == INVALID
+
+
+def test_tree_rejects_bad_shape_and_null_prefix():
+    lib = capi.load()
+    assert lib.bc_tree_verify(_shape(dim=80), _tree_inputs(), 7, None) == INVALID
+    ins = _tree_inputs()
+    ins.prefix.k = None
+    assert lib.bc_tree_verify(_shape(), ins, 7, None) == INVALID
+
+
+@pytest.mark.parametrize("request_,nodes,accepted", [(-1, 7, 1), (2, 7, 1), (0, 0, 1),
+                                                     (0, 7, 0), (0, 7, 8)])
+def test_commit_rejects(request_, nodes, accepted):
+    lib = capi.load()
+    s = capi.Shape(2, 8, 8, 128, 1, 16)
+    assert lib.bc_commit_path(s, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, request_, nodes,
+                              accepted, None) == INVALID
+    assert lib.bc_commit_path(capi.Shape(2, 8, 8, 96, 1, 16), FAKE, FAKE, FAKE, FAKE, FAKE,
+                              FAKE, FAKE, 0, 7, 1, None) == INVALID
+
+
+def test_copy_pages_rejects():
+    lib = capi.load()
+    s = capi.Shape(1, 8, 8, 128, 1, 16)
+    assert lib.bc_copy_pages(s, None, FAKE, FAKE, FAKE, 1, None) == INVALID
+    assert lib.bc_copy_pages(s, FAKE, FAKE, FAKE, FAKE, -1, None) == INVALID
+    assert lib.bc_copy_pages(s, FAKE, FAKE, FAKE, FAKE, 0, None) == capi.BC_SUCCESS
+
+
+@pytest.mark.parametrize("strides,scale", [((0, 1, 1, 1), 0.1), ((1, 0, 1, 1), 0.1),
+                                           ((1, 1, 0, 1), 0.1), ((1, 1, 1, 0), 0.1),
+                                           ((8, 8, 8, 8), 0.0), ((8, 8, 8, 8), -1.0),
+                                           ((8, 8, 8, 8), float("nan"))])
+def test_packed_rejects(strides, scale):
+    lib = capi.load()
+    s = _shape()
+    assert lib.bc_packed_decode(s, FAKE, FAKE, FAKE, FAKE, FAKE, *strides, scale,
+                                None) == INVALID
+    assert lib.bc_packed_decode_ws(s, FAKE, FAKE, FAKE, FAKE, FAKE, *strides, scale, None, 0,
+                                   None) == INVALID
+
+
+def test_auto_splits_policy():
+    lib = capi.load()
+    # contexts below 512 tokens stay unsplit (src/paged_gqa.cu:211)
+    assert lib.bc_auto_splits(_shape(batch=1), 511, 256) == 1
+    # long context, low batch: many splits, at least 128 tokens each, powers of 2
+    s4 = lib.bc_auto_splits(_shape(batch=4), 32768, 256)
+    assert s4 >= 16 and s4 & (s4 - 1) == 0 and 32768 // s4 >= 128
+    # large batches need no split to fill 256 CUs
+    assert lib.bc_auto_splits(_shape(batch=512), 4096, 256) == 1
+    for ctx in (512, 1000, 4096, 100000):
+        s = lib.bc_auto_splits(_shape(batch=1), ctx, 256)
+        assert 1 <= s <= capi.BC_MAX_SPLITS and ctx // s >= 128
+
+
+def test_workspace_sizes():
+    lib = capi.load()
+    c5 = capi.Shape(64, 32, 8, 128, 256, 20000)
+    assert lib.bc_packed_decode_workspace_size(c5) > 0
+    assert lib.bc_packed_decode_workspace_size(capi.Shape(4, 32, 8, 128, 8, 64)) == 0
+    assert lib.bc_packed_decode_workspace_size(capi.Shape(4, 32, 8, 96, 8, 64)) == 0
+    c3 = capi.Shape(8, 32, 8, 128, 129, 160)
+    assert lib.bc_tree_verify_workspace_size(c3, 7) > 0
+    assert lib.bc_tree_verify_workspace_size(c3, 0) == 0
+
+
+def test_torch_ops_register_reference_schemas():
+    """The op library loads on a GPU-less host and registers the reference's
+    schemas verbatim (bindings/torch_ops.cpp:144-148)."""
+    import torch
+    import branchcraft_torch  # noqa: F401
+
+    want = {
+        "tree_verify": "branchcraft::tree_verify(Tensor q, Tensor prefix_k, Tensor prefix_v, "
+                       "Tensor pages, Tensor lengths, Tensor draft_k, Tensor draft_v, "
+                       "Tensor parent) -> Tensor",
+        "packed_decode_out": "branchcraft::packed_decode_out(Tensor q, Tensor packed_kv, "
+                             "Tensor pages, Tensor lengths, Tensor(a!) output, float scale) "
+                             "-> Tensor(a!)",
+        "commit_path_": "branchcraft::commit_path_(Tensor(a!) cache_k, Tensor(b!) cache_v, "
+                        "Tensor draft_k, Tensor draft_v, Tensor path_nodes, "
+                        "Tensor dest_pages, Tensor dest_slots, int request) -> ()",
+    }
+    for name, schema in want.items():
+        assert str(getattr(torch.ops.branchcraft, name).default._schema) == schema
+
+
+def test_ops_have_no_cpu_fallback():
+    import torch
+    import branchcraft_torch as bc
+
+    q = torch.zeros(1, 1, 4, 64, dtype=torch.float16)
+    k = torch.zeros(1, 16, 2, 64, dtype=torch.float16)
+    pages = torch.zeros(1, 1, dtype=torch.int32)
+    with pytest.raises((NotImplementedError, RuntimeError)):
+        bc.tree_verify(q, k, k, pages, torch.zeros(1, dtype=torch.int32),
+                       torch.zeros(1, 1, 2, 64, dtype=torch.float16),
+                       torch.zeros(1, 1, 2, 64, dtype=torch.float16),
+                       torch.full((1, 1), -1, dtype=torch.int32))
