@@ -7,9 +7,15 @@
 // (src/packed_decode.cu:15-60).  The reference runs one 32-lane warp per
 // query head and walks tokens serially with a shuffle reduction per token.
 //
-// Here a workgroup owns one (sequence, token range) and holds one wave64
-// per KV head (up to eight), so the waves together stream every page of the
-// range as whole 16-slot blocks.  Inside a wave, one 16-token page and the
+// A workgroup holds one wave64 per KV head (up to eight) and walks a flat
+// range of pages, so the waves together stream every page as whole 16-slot
+// blocks.  The range is either one whole sequence or, for split decode, an
+// equal share of all the batch's pages: workgroup w of W takes pages
+// [w*T/W, (w+1)*T/W) of the concatenated sequences, crossing sequence
+// boundaries as it goes, so every workgroup does the same work however
+// ragged the lengths are.  A sequence that ends inside one workgroup's
+// range is written directly; the others leave an FP32 partial (max, sum,
+// acc) per workgroup and a merge kernel combines them.  Inside a wave, one 16-token page and the
 // query heads of one KV head (the GQA group, up to 16) form MFMA tiles:
 //
 //   S^T[16 tok x 16 heads] = K[16 tok x D] . Q^T[D x 16 heads]
@@ -31,6 +37,8 @@
 
 #include <math.h>
 
+#include <atomic>
+
 namespace {
 
 using namespace bcd;
@@ -50,8 +58,8 @@ struct AttnParams {
   const int32_t* pages;   // [B, max_pages]
   const int32_t* lengths; // [B]
   void* out;              // [B, Hq, D], float or _Float16
-  float* part_acc;        // split partials: acc
-  float* part_ml;         // split partials: (max, sum), max in log2 units
+  float* part_acc;        // partials [slot][Hq][D], slot = workgroup + sequence
+  float* part_ml;         // partials [slot][Hq][2]: (max in log2 units, sum)
   long long page_stride;  // elements between physical pages
   long long head_stride;  // elements between KV heads
   long long slot_stride;  // elements between page slots
@@ -59,17 +67,68 @@ struct AttnParams {
   int zdim;               // head blocks per sequence = hkv * nblk
   int waves;              // waves per workgroup (head blocks per workgroup)
   float scale_log2;       // softmax scale * log2(e)
-  int splits;             // > 0: `splits` equal partitions per sequence
-  int chunk_tokens;       // splits == 0: fixed chunks of this many tokens
-  int max_chunks;         // chunk rows reserved per (b, h) in chunk mode
+  int nwg;                // > 0: flat page ranges over nwg workgroups;
+                          // 0: one workgroup per sequence
 };
 
-// Row index of a partial state.  Split mode keeps the reference's scratch
-// layout, row = (part*B + b)*Hq + h (src/paged_gqa.cu:141).
-__device__ __forceinline__ int partial_row(const AttnParams& P, int part, int b,
-                                           int h) {
-  return P.splits > 0 ? (part * P.batch + b) * P.hq + h
-                      : (b * P.hq + h) * P.max_chunks + part;
+__device__ __forceinline__ int seq_len(const AttnParams& P, int b) {
+  return max(0, min(P.lengths[b], P.max_pages * BC_PAGE_SIZE));
+}
+
+__device__ __forceinline__ int seq_pages(const AttnParams& P, int b) {
+  return (seq_len(P, b) + BC_PAGE_SIZE - 1) / BC_PAGE_SIZE;
+}
+
+__device__ __forceinline__ int wave_sum_i(int x) {
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) x += __shfl_xor(x, off, 64);
+  return x;
+}
+
+__device__ __forceinline__ int wave_incl_scan_i(int x, int lane) {
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int y = __shfl_up(x, off, 64);
+    if (lane >= off) x += y;
+  }
+  return x;
+}
+
+// Total pages of the batch and the page count per workgroup (flat mode).
+__device__ void flat_geometry(const AttnParams& P, int lane, int& total, int& per) {
+  int t = 0;
+  for (int base = 0; base < P.batch; base += 64)
+    t += wave_sum_i(base + lane < P.batch ? seq_pages(P, base + lane) : 0);
+  total = t;
+  per = (t + P.nwg - 1) / P.nwg;
+}
+
+// Pages of the sequences before b.
+__device__ int pages_before(const AttnParams& P, int lane, int b) {
+  int t = 0;
+  for (int base = 0; base < b; base += 64)
+    t += wave_sum_i(base + lane < b ? seq_pages(P, base + lane) : 0);
+  return t;
+}
+
+// Sequence holding flat page f (f < total) and the flat index of its first page.
+__device__ void locate(const AttnParams& P, int lane, int f, int& b, int& start) {
+  int run = 0;
+  for (int base = 0; base < P.batch; base += 64) {
+    const int n = base + lane < P.batch ? seq_pages(P, base + lane) : 0;
+    const int inc = wave_incl_scan_i(n, lane);
+    const int tot = __builtin_amdgcn_readlane(inc, 63);
+    if (run + tot > f) {
+      const unsigned long long hit = __builtin_amdgcn_ballot_w64(run + inc > f);
+      const int first = __builtin_ffsll((long long)hit) - 1;
+      b = base + first;
+      start = run + __builtin_amdgcn_readlane(inc - n, first);
+      return;
+    }
+    run += tot;
+  }
+  b = P.batch - 1;
+  start = run;
 }
 
 template <typename OutT>
@@ -123,180 +182,213 @@ __global__ __launch_bounds__(64 * kMaxWaves) void paged_attn_kernel(AttnParams P
   const int g4 = lane >> 4;   // k-slice group / output row group
   const int c16 = lane & 15;  // token row of A, head column of B and C
 
-  // blockIdx.x = (zg * batch + b) * parts + part; wave -> head block z.
-  const int parts = P.splits > 0 ? P.splits : P.max_chunks;
-  const int part = blockIdx.x % parts;
-  const int zb = blockIdx.x / parts;
-  const int b = zb % P.batch;
-  const int z = (zb / P.batch) * P.waves + wave;
+  // blockIdx.x = range * zgroups + zg; wave -> head block z.
+  const int zgroups = (P.zdim + P.waves - 1) / P.waves;
+  const int zg = blockIdx.x % zgroups;
+  const int rid = blockIdx.x / zgroups;
+  const int z = zg * P.waves + wave;
   if (z >= P.zdim) return;  // no workgroup barrier below
   const int kvh = z / P.nblk;
   const int h0 = kvh * P.group + (z % P.nblk) * kHeadCols;
   const int nh = min(kHeadCols, P.group - (z % P.nblk) * kHeadCols);
+  const float c = P.scale_log2;
 
-  const int len = max(0, min(P.lengths[b], P.max_pages * BC_PAGE_SIZE));
-  int begin, end;
-  bool final_out;
-  if (P.splits > 0) {
-    const int chunk = (len + P.splits - 1) / P.splits;
-    begin = min(part * chunk, len);
-    end = min(begin + chunk, len);
-    final_out = P.splits == 1;
+  // This workgroup's pages: sequence pb from local page `plocal`, `count`
+  // pages in all (crossing into later sequences in flat mode).
+  int pb, plocal, count;
+  if (P.nwg == 0) {
+    pb = rid;
+    plocal = 0;
+    count = seq_pages(P, pb);
+    if (count == 0) {  // empty sequence: zeros (src/paged_gqa.cu:63)
+      if (c16 < nh) {
+        const size_t o = ((size_t)pb * P.hq + h0 + c16) * D + 4 * g4;
+#pragma unroll
+        for (int t = 0; t < DT; ++t) store4<OutT>(P.out, o + 16 * t, 0.f, 0.f, 0.f, 0.f);
+      }
+      return;
+    }
   } else {
-    const int nchunks = max(1, (len + P.chunk_tokens - 1) / P.chunk_tokens);
-    if (part >= nchunks) return;
-    begin = part * P.chunk_tokens;
-    end = min(begin + P.chunk_tokens, len);
-    final_out = nchunks == 1;
+    int total, per;
+    flat_geometry(P, lane, total, per);
+    const int f0 = rid * per;
+    const int f1 = min(total, f0 + per);
+    if (f0 >= f1) return;
+    int start;
+    locate(P, lane, f0, pb, start);
+    plocal = f0 - start;
+    count = f1 - f0;
   }
+  int ppages = seq_pages(P, pb);
+  int plen = seq_len(P, pb);
+  int seg0 = plocal;  // first local page of pb in this range
 
   // Q^T B operand: lane holds Q[head h0+c16][32s + 8*g4 .. +8].
   uint4 qB[KS];
-  {
+  auto load_q = [&](int b) {
     const uint16_t* qp = P.q + ((size_t)b * P.hq + h0 + c16) * D + 8 * g4;
 #pragma unroll
     for (int s = 0; s < KS; ++s)
       qB[s] = c16 < nh ? load8<VEC>(qp + 32 * s) : make_uint4(0, 0, 0, 0);
-  }
+  };
+  load_q(pb);
 
-  const float c = P.scale_log2;
   f32x4 acc[DT];
 #pragma unroll
   for (int t = 0; t < DT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m = kNegInf, l = 0.f;  // head c16; m is the running max of raw scores
 
+  // acc[t][j] = O^T[dim 16t + 4*g4 + j][head h0 + c16]
+  auto finalize = [&](bool complete) {
+    float lt = l + shfl_xor_f(l, 16);  // each lane summed its own 4 token rows
+    lt += shfl_xor_f(lt, 32);
+    if (c16 >= nh) return;
+    const int h = h0 + c16;
+    if (complete) {
+      const float inv = lt > 0.f ? 1.f / lt : 0.f;
+      const size_t o = ((size_t)pb * P.hq + h) * D + 4 * g4;
+#pragma unroll
+      for (int t = 0; t < DT; ++t)
+        store4<OutT>(P.out, o + 16 * t, acc[t][0] * inv, acc[t][1] * inv,
+                     acc[t][2] * inv, acc[t][3] * inv);
+    } else {
+      const size_t r = (size_t)(rid + pb) * P.hq + h;
+      float* pa = P.part_acc + r * D + 4 * g4;
+#pragma unroll
+      for (int t = 0; t < DT; ++t)
+        *reinterpret_cast<float4*>(pa + 16 * t) =
+            make_float4(acc[t][0], acc[t][1], acc[t][2], acc[t][3]);
+      if (g4 == 0) {
+        P.part_ml[2 * r] = m == kNegInf ? kNegInf : m * c;
+        P.part_ml[2 * r + 1] = lt;
+      }
+    }
+  };
+
   _Float16* vs = s_v + wave * 16 * VP;
   // Transpose-read address: lane (g4, c16) names [token 4*g4 + c16/4][4*(c16%4)].
   const _Float16* vtr = vs + (4 * g4 + (c16 >> 2)) * VP + 4 * (c16 & 3);
+  const long long lane_off =
+      (long long)kvh * P.head_stride + (long long)c16 * P.slot_stride + 8 * g4;
 
-  if (end > begin) {
-    const int pfirst = begin / BC_PAGE_SIZE;
-    const int npg = (end - 1) / BC_PAGE_SIZE - pfirst + 1;
-    const int32_t* prow = P.pages + (size_t)b * P.max_pages + pfirst;
-    const long long lane_off =
-        (long long)kvh * P.head_stride + (long long)c16 * P.slot_stride + 8 * g4;
-
-    // Page ids are scalar loads (counted by lgkmcnt, not vmcnt), fetched one
-    // iteration before the K/V loads that use them, so waiting for an id
-    // never waits for the K/V prefetches in flight.
-    // Issues past the range re-read the range's last page (an L2 hit), so
-    // every path through the loop has the same loads in flight and the
-    // compiler's vmcnt waits stay two pages deep.
-    auto page_id = [&](int r) -> int { return prow[r < npg ? r : npg - 1]; };
-
-    auto issue = [&](int phys, uint4 (&kb)[KS], uint4 (&vb)[KS], bool& valid) {
-      valid = phys >= 0 && phys < P.phys_pages;
-      const long long base = (valid ? (long long)phys : 0ll) * P.page_stride + lane_off;
-#pragma unroll
-      for (int s = 0; s < KS; ++s) kb[s] = load8<VEC>(P.kbase + base + 32 * s);
-#pragma unroll
-      for (int s = 0; s < KS; ++s) vb[s] = load8<VEC>(P.vbase + base + 32 * s);
-    };
-
-    auto process = [&](int r, const uint4 (&kb)[KS], uint4 (&vb)[KS], bool valid) {
-      const int t0 = (pfirst + r) * BC_PAGE_SIZE;
-      const bool full = valid && t0 >= begin && t0 + BC_PAGE_SIZE <= end;
-      if (!full) {
-        // Slots outside the range may hold any bits (NaN included); their
-        // weight is zero, so their V row must be zero too.
-        const int t = t0 + c16;
-        if (!(valid && t >= begin && t < end)) {
-#pragma unroll
-          for (int s = 0; s < KS; ++s) vb[s] = make_uint4(0, 0, 0, 0);
-        }
-      }
-      f32x4 sc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int s = 0; s < KS; ++s)
-        sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, kb[s]),
-                                                   __builtin_bit_cast(f16x8, qB[s]),
-                                                   sc, 0, 0, 0);
-      // Stage V while the MFMAs drain.
-#pragma unroll
-      for (int s = 0; s < KS; ++s)
-        *reinterpret_cast<uint4*>(vs + c16 * VP + 32 * s + 8 * g4) = vb[s];
-
-      float sv[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int t = t0 + 4 * g4 + j;
-        sv[j] = (full || (valid && t >= begin && t < end)) ? sc[j] : kNegInf;
-      }
-      float tmax = __builtin_fmaxf(__builtin_fmaxf(sv[0], sv[1]), __builtin_fmaxf(sv[2], sv[3]));
-      tmax = __builtin_fmaxf(tmax, shfl_xor_f(tmax, 16));
-      tmax = __builtin_fmaxf(tmax, shfl_xor_f(tmax, 32));
-      const float mnew = __builtin_fmaxf(m, tmax);
-      if (__builtin_amdgcn_ballot_w64(mnew > m)) {
-        const float alpha = fast_exp2((m - safe_max(mnew)) * c);
-        l *= alpha;
-#pragma unroll
-        for (int t = 0; t < DT; ++t) acc[t] *= alpha;
-        m = mnew;
-      }
-      const float mc = safe_max(m) * c;
-      f16x4 ph, pl;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float pr = fast_exp2(__builtin_fmaf(sv[j], c, -mc));
-        l += pr;
-        ph[j] = (_Float16)pr;
-        pl[j] = (_Float16)(pr - (float)ph[j]);
-      }
-      wave_lds_sync();
-#pragma unroll
-      for (int t = 0; t < DT; ++t) {
-        const f16x4 a = lds_read_tr(vtr + 16 * t);
-        acc[t] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, ph, acc[t], 0, 0, 0);
-        acc[t] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, pl, acc[t], 0, 0, 0);
-      }
-      wave_lds_sync();
-    };
-
-    uint4 ka[KS], va[KS], kb2[KS], vb2[KS], kc[KS], vc[KS];
-    bool oka = false, okb = false, okc = false;
-    issue(page_id(0), ka, va, oka);
-    issue(page_id(1), kb2, vb2, okb);
-    int nid = page_id(2);  // id of the next page to issue
-    for (int r = 0; r < npg; r += 3) {
-      issue(nid, kc, vc, okc);
-      nid = page_id(r + 3);
-      process(r, ka, va, oka);
-      if (r + 1 >= npg) break;
-      issue(nid, ka, va, oka);
-      nid = page_id(r + 4);
-      process(r + 1, kb2, vb2, okb);
-      if (r + 2 >= npg) break;
-      issue(nid, kb2, vb2, okb);
-      nid = page_id(r + 5);
-      process(r + 2, kc, vc, okc);
+  // Issue cursor: walks the same pages ahead of the compute cursor.  Page
+  // ids are scalar loads (counted by lgkmcnt, not vmcnt), fetched one step
+  // before the K/V loads that use them; issues past the range repeat the
+  // last page (an L2 hit), so every path has the same loads in flight.
+  int ib = pb, ilocal = plocal, ipages = ppages, issued = 0, last_phys = 0;
+  auto next_id = [&]() -> int {
+    if (issued >= count) return last_phys;
+    last_phys = P.pages[(size_t)ib * P.max_pages + ilocal];
+    ++issued;
+    if (++ilocal == ipages && issued < count) {
+      do {
+        ++ib;
+        ipages = seq_pages(P, ib);
+      } while (ipages == 0);
+      ilocal = 0;
     }
-  }
+    return last_phys;
+  };
 
-  // Each lane summed the weights of its own four token rows; add the groups.
-  l += shfl_xor_f(l, 16);
-  l += shfl_xor_f(l, 32);
-  if (c16 >= nh) return;
-  const int h = h0 + c16;
-  // acc[t][j] = O^T[dim 16t + 4*g4 + j][head h]
-  if (final_out) {
-    const float inv = l > 0.f ? 1.f / l : 0.f;
-    const size_t o = ((size_t)b * P.hq + h) * D + 4 * g4;
+  auto issue = [&](int phys, uint4 (&kb)[KS], uint4 (&vb)[KS], bool& valid) {
+    valid = phys >= 0 && phys < P.phys_pages;
+    const long long base = (valid ? (long long)phys : 0ll) * P.page_stride + lane_off;
 #pragma unroll
-    for (int t = 0; t < DT; ++t)
-      store4<OutT>(P.out, o + 16 * t, acc[t][0] * inv, acc[t][1] * inv, acc[t][2] * inv,
-                   acc[t][3] * inv);
-  } else {
-    const size_t r = partial_row(P, part, b, h);
-    float* pa = P.part_acc + r * D + 4 * g4;
+    for (int s = 0; s < KS; ++s) kb[s] = load8<VEC>(P.kbase + base + 32 * s);
 #pragma unroll
-    for (int t = 0; t < DT; ++t)
-      *reinterpret_cast<float4*>(pa + 16 * t) =
-          make_float4(acc[t][0], acc[t][1], acc[t][2], acc[t][3]);
-    if (g4 == 0) {
-      P.part_ml[2 * r] = m == kNegInf ? kNegInf : m * c;
-      P.part_ml[2 * r + 1] = l;
+    for (int s = 0; s < KS; ++s) vb[s] = load8<VEC>(P.vbase + base + 32 * s);
+  };
+
+  auto process = [&](int idx, const uint4 (&kb)[KS], uint4 (&vb)[KS], bool valid) {
+    if (idx >= count) return;  // padding step: loop bodies never exit early
+    const int t0 = plocal * BC_PAGE_SIZE;
+    const bool full = valid && t0 + BC_PAGE_SIZE <= plen;
+    if (!full) {
+      // Slots past the length may hold any bits (NaN included); their weight
+      // is zero, so their V row must be zero too.
+      if (!(valid && t0 + c16 < plen)) {
+#pragma unroll
+        for (int s = 0; s < KS; ++s) vb[s] = make_uint4(0, 0, 0, 0);
+      }
     }
+    f32x4 sc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+      sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, kb[s]),
+                                                 __builtin_bit_cast(f16x8, qB[s]),
+                                                 sc, 0, 0, 0);
+    // Stage V while the MFMAs drain.
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+      *reinterpret_cast<uint4*>(vs + c16 * VP + 32 * s + 8 * g4) = vb[s];
+
+    float sv[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      sv[j] = (full || (valid && t0 + 4 * g4 + j < plen)) ? sc[j] : kNegInf;
+    float tmax = __builtin_fmaxf(__builtin_fmaxf(sv[0], sv[1]), __builtin_fmaxf(sv[2], sv[3]));
+    tmax = __builtin_fmaxf(tmax, shfl_xor_f(tmax, 16));
+    tmax = __builtin_fmaxf(tmax, shfl_xor_f(tmax, 32));
+    const float mnew = __builtin_fmaxf(m, tmax);
+    if (__builtin_amdgcn_ballot_w64(mnew > m)) {
+      const float alpha = fast_exp2((m - safe_max(mnew)) * c);
+      l *= alpha;
+#pragma unroll
+      for (int t = 0; t < DT; ++t) acc[t] *= alpha;
+      m = mnew;
+    }
+    const float mc = safe_max(m) * c;
+    f16x4 ph, pl;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float pr = fast_exp2(__builtin_fmaf(sv[j], c, -mc));
+      l += pr;
+      ph[j] = (_Float16)pr;
+      pl[j] = (_Float16)(pr - (float)ph[j]);
+    }
+    wave_lds_sync();
+#pragma unroll
+    for (int t = 0; t < DT; ++t) {
+      const f16x4 a = lds_read_tr(vtr + 16 * t);
+      acc[t] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, ph, acc[t], 0, 0, 0);
+      acc[t] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, pl, acc[t], 0, 0, 0);
+    }
+    wave_lds_sync();
+
+    if (++plocal == ppages) {
+      // Sequence pb ends inside this range.
+      finalize(seg0 == 0);
+      if (idx + 1 < count) {
+        do {
+          ++pb;
+          ppages = seq_pages(P, pb);
+        } while (ppages == 0);
+        plen = seq_len(P, pb);
+        plocal = 0;
+        seg0 = 0;
+        load_q(pb);
+#pragma unroll
+        for (int t = 0; t < DT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+        m = kNegInf;
+        l = 0.f;
+      }
+    }
+  };
+
+  uint4 ka[KS], va[KS], kb2[KS], vb2[KS];
+  bool oka = false, okb = false;
+  issue(next_id(), ka, va, oka);
+  int nid = next_id();
+  for (int idx = 0; idx < count; idx += 2) {
+    issue(nid, kb2, vb2, okb);
+    nid = next_id();
+    process(idx, ka, va, oka);
+    issue(nid, ka, va, oka);
+    nid = next_id();
+    process(idx + 1, kb2, vb2, okb);
   }
+  // The range ended inside sequence pb: leave a partial.
+  if (plocal != ppages) finalize(false);
 }
 
 __device__ __forceinline__ float wave_max(float x) {
@@ -311,11 +403,11 @@ __device__ __forceinline__ float wave_sum(float x) {
   return x;
 }
 
-// out = sum_p 2^(m_p - M) a_p / sum_p 2^(m_p - M) l_p over a sequence's
-// partials; all-empty rows give zeros (src/paged_gqa.cu:76-106).  One wave
-// per (b, h) output row: lane p reads partial p's (max, sum), the weights are
-// formed once, then every lane accumulates its dims over the partials with
-// independent loads.
+// Flat mode: out = sum_w 2^(m_w - M) a_w / sum_w 2^(m_w - M) l_w over the
+// workgroups whose ranges cut sequence b (src/paged_gqa.cu:76-106); empty
+// sequences give zeros.  One wave per (b, h) output row: lane i reads
+// partial i's (max, sum), the weights are formed once, then every lane
+// accumulates its dims over the partials with independent loads.
 template <int D, typename OutT>
 __global__ __launch_bounds__(256) void merge_kernel(AttnParams P) {
   constexpr int PER = D / 64;
@@ -323,22 +415,25 @@ __global__ __launch_bounds__(256) void merge_kernel(AttnParams P) {
   const int rowi = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (rowi >= P.batch * P.hq) return;
   const int b = rowi / P.hq, h = rowi % P.hq;
-  int nparts;
-  if (P.splits > 0) {
-    nparts = P.splits;
-  } else {
-    const int len = max(0, min(P.lengths[b], P.max_pages * BC_PAGE_SIZE));
-    nparts = (len + P.chunk_tokens - 1) / P.chunk_tokens;
-    if (nparts <= 1) return;  // written directly by the attention kernel
+  const int np = seq_pages(P, b);
+  if (np == 0) {
+#pragma unroll
+    for (int j = 0; j < PER; ++j) store_out<OutT>(P.out, (size_t)rowi * D + lane + 64 * j, 0.f);
+    return;
   }
+  int total, per;
+  flat_geometry(P, lane, total, per);
+  const int start = pages_before(P, lane, b);
+  const int w0 = start / per, w1 = (start + np - 1) / per;
+  if (w0 == w1) return;  // the sequence ended inside one range: written directly
   float mm = kNegInf, lsum = 0.f, a[PER];
 #pragma unroll
   for (int j = 0; j < PER; ++j) a[j] = 0.f;
-  for (int p0 = 0; p0 < nparts; p0 += 64) {
-    const int cnt = min(64, nparts - p0);
+  for (int wb = w0; wb <= w1; wb += 64) {
+    const int cnt = min(64, w1 - wb + 1);
     float mp = kNegInf, lp = 0.f;
     if (lane < cnt) {
-      const size_t r = partial_row(P, p0 + lane, b, h);
+      const size_t r = (size_t)(wb + lane + b) * P.hq + h;
       mp = P.part_ml[2 * r];
       lp = P.part_ml[2 * r + 1];
     }
@@ -354,7 +449,7 @@ __global__ __launch_bounds__(256) void merge_kernel(AttnParams P) {
     for (int i = 0; i < cnt; ++i) {
       const float wi = __builtin_bit_cast(float, __builtin_amdgcn_readlane(
                                                      __builtin_bit_cast(int, w), i));
-      const float* src = P.part_acc + (size_t)partial_row(P, p0 + i, b, h) * D + lane;
+      const float* src = P.part_acc + ((size_t)(wb + i + b) * P.hq + h) * D + lane;
 #pragma unroll
       for (int j = 0; j < PER; ++j) a[j] += wi * src[64 * j];
     }
@@ -364,6 +459,10 @@ __global__ __launch_bounds__(256) void merge_kernel(AttnParams P) {
   for (int j = 0; j < PER; ++j)
     store_out<OutT>(P.out, (size_t)rowi * D + lane + 64 * j, a[j] * inv);
 }
+
+}  // namespace
+
+namespace {
 
 bool shape_ok(const bc_shape& s) {
   return s.batch >= 1 && s.query_heads >= 1 && s.kv_heads >= 1 &&
@@ -377,14 +476,14 @@ void launch_attn(const AttnParams& P, dim3 grid, hipStream_t st) {
 }
 
 template <int D, typename OutT>
-hipError_t launch_dim(const AttnParams& P, int parts, bool vec, hipStream_t st) {
+hipError_t launch_dim(const AttnParams& P, bool vec, hipStream_t st) {
   const int zgroups = (P.zdim + P.waves - 1) / P.waves;
-  const dim3 grid((unsigned)((size_t)parts * P.batch * zgroups));
+  const int ranges = P.nwg > 0 ? P.nwg : P.batch;
+  const dim3 grid((unsigned)((size_t)ranges * zgroups));
   if (vec) launch_attn<D, OutT, true>(P, grid, st);
   else launch_attn<D, OutT, false>(P, grid, st);
   hipError_t err = hipGetLastError();
-  const bool need_merge = P.splits > 0 ? P.splits > 1 : P.max_chunks > 1;
-  if (err != hipSuccess || !need_merge) return err;
+  if (err != hipSuccess || P.nwg == 0) return err;
   const unsigned rows = (unsigned)P.batch * P.hq;
   merge_kernel<D, OutT><<<dim3((rows + 3) / 4), 256, 0, st>>>(P);
   return hipGetLastError();
@@ -395,7 +494,7 @@ bool aligned16(const void* p) {
 }
 
 template <typename OutT>
-hipError_t launch(AttnParams& P, int dim, int parts, hipStream_t st) {
+hipError_t launch(AttnParams& P, int dim, hipStream_t st) {
   P.group = P.hq / P.hkv;
   P.nblk = (P.group + kHeadCols - 1) / kHeadCols;
   P.zdim = P.hkv * P.nblk;
@@ -403,30 +502,57 @@ hipError_t launch(AttnParams& P, int dim, int parts, hipStream_t st) {
   const bool vec = aligned16(P.q) && aligned16(P.kbase) &&
                    aligned16(P.vbase) &&
                    (P.page_stride | P.head_stride | P.slot_stride) % 8 == 0;
-  return dim == 64 ? launch_dim<64, OutT>(P, parts, vec, st)
-                   : launch_dim<128, OutT>(P, parts, vec, st);
+  return dim == 64 ? launch_dim<64, OutT>(P, vec, st)
+                   : launch_dim<128, OutT>(P, vec, st);
 }
 
-// Packed decode splits sequences into chunks of this many tokens when a
-// workspace is supplied; a row shorter than one chunk runs unsplit.
-#ifndef BC_PACKED_CHUNK_TOKENS
-#define BC_PACKED_CHUNK_TOKENS 256
-#endif
-int packed_chunk_tokens(const bc_shape& s) {
-  const int max_tokens = s.max_pages * BC_PAGE_SIZE;
-  return max_tokens > BC_PACKED_CHUNK_TOKENS ? BC_PACKED_CHUNK_TOKENS : max_tokens;
+// Compute units of the current device (cached per device; an immutable
+// attribute, so the cache is safe to share between threads).
+int device_cus() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 256;
+  if (dev < 64) {
+    const int v = cache[dev].load(std::memory_order_relaxed);
+    if (v > 0) return v;
+  }
+  int n = 0;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      n < 1)
+    n = 256;
+  if (dev < 64) cache[dev].store(n, std::memory_order_relaxed);
+  return n;
 }
 
-size_t packed_workspace(const bc_shape& s, int* chunk_tokens, int* max_chunks) {
-  const int ct = packed_chunk_tokens(s);
-  const int mc = (s.max_pages * BC_PAGE_SIZE + ct - 1) / ct;
-  if (chunk_tokens) *chunk_tokens = ct;
-  if (max_chunks) *max_chunks = mc;
-  if (mc <= 1) return 0;
-  const size_t rows = (size_t)s.batch * s.query_heads * mc;
-  const size_t acc = rows * s.dim * sizeof(float);
-  const size_t ml = rows * 2 * sizeof(float);
-  return ((acc + 255) & ~(size_t)255) + ml;
+// Flat-mode workgroup count for a given number of partial slots per head:
+// slot = workgroup + sequence must stay below `slots`, and a whole number of
+// waves of workgroups over the CUs (one 8-wave workgroup per CU) balances best.
+int flat_workgroups(int batch, long long slots, int cus, int zgroups) {
+  long long nwg = slots - batch + 1;
+  const long long per_wave = cus / (zgroups > 0 ? zgroups : 1);
+  if (per_wave >= 1 && nwg > per_wave) nwg = nwg / per_wave * per_wave;
+  if (nwg < 1) nwg = 1;
+  return (int)nwg;
+}
+
+int zgroups_of(const bc_shape& s) {
+  const int group = s.query_heads / s.kv_heads;
+  const int zdim = s.kv_heads * ((group + kHeadCols - 1) / kHeadCols);
+  const int waves = zdim < kMaxWaves ? zdim : kMaxWaves;
+  return (zdim + waves - 1) / waves;
+}
+
+// Packed decode with a workspace: flat ranges over one workgroup per CU.
+int packed_nwg(const bc_shape& s) {
+  const int zg = zgroups_of(s);
+  int n = device_cus() / zg;
+  return n < 1 ? 1 : n;
+}
+
+size_t packed_workspace(const bc_shape& s, int nwg) {
+  const size_t slots = (size_t)nwg + s.batch;
+  const size_t acc = (slots * s.query_heads * s.dim * sizeof(float) + 255) & ~(size_t)255;
+  return acc + slots * s.query_heads * 2 * sizeof(float);
 }
 
 }  // namespace
@@ -455,30 +581,31 @@ extern "C" int bc_decode(bc_shape s, bc_inputs in, bc_scratch scratch,
   P.max_pages = s.max_pages;
   P.phys_pages = s.physical_pages;
   P.scale_log2 = (float)(kLog2e / sqrt((double)s.dim));
-  P.splits = splits;
-  return launch<float>(P, s.dim, splits, reinterpret_cast<hipStream_t>(stream));
+  // splits == 1: one workgroup per sequence.  splits > 1: flat ranges whose
+  // partial slots fit the caller's splits*B*Hq rows.
+  P.nwg = splits == 1 ? 0
+                      : flat_workgroups(s.batch, (long long)splits * s.batch, device_cus(),
+                                        zgroups_of(s));
+  return launch<float>(P, s.dim, reinterpret_cast<hipStream_t>(stream));
 }
 
 extern "C" int bc_auto_splits(bc_shape s, int max_length, int cu_count) {
-  // One workgroup covers up to eight KV-head blocks of one sequence range.
-  // Aim for about two workgroups per CU, keep at least 128 tokens per split
-  // and leave contexts under 512 tokens unsplit.
-  if (max_length < 512 || s.batch < 1 || s.kv_heads < 1 || s.query_heads < 1 ||
+  // Split decode runs flat page ranges: (splits - 1) * batch + 1 workgroups
+  // share all pages equally.  Pick the largest split count whose workgroups
+  // fit one per CU; contexts under 64 tokens stay in one workgroup.
+  if (max_length < 64 || s.batch < 1 || s.kv_heads < 1 || s.query_heads < 1 ||
       s.query_heads % s.kv_heads)
     return 1;
-  const int group = s.query_heads / s.kv_heads;
-  const long long zdim = (long long)s.kv_heads * ((group + kHeadCols - 1) / kHeadCols);
-  const long long base = (long long)s.batch * ((zdim + kMaxWaves - 1) / kMaxWaves);
-  const long long wanted = (2ll * (cu_count > 0 ? cu_count : 256) + base - 1) / base;
-  int splits = 1;
-  while (splits < wanted && splits < BC_MAX_SPLITS) splits *= 2;
-  while (splits > 1 && max_length / splits < 128) splits /= 2;
-  return splits;
+  const int cus = cu_count > 0 ? cu_count : 256;
+  const int per_wave = cus / zgroups_of(s);
+  long long splits = per_wave > 1 ? (per_wave - 1) / s.batch + 1 : 1;
+  if (splits > BC_MAX_SPLITS) splits = BC_MAX_SPLITS;
+  return (int)splits;
 }
 
 extern "C" size_t bc_packed_decode_workspace_size(bc_shape s) {
   if (!shape_ok(s)) return 0;
-  return packed_workspace(s, nullptr, nullptr);
+  return packed_workspace(s, packed_nwg(s));
 }
 
 static int packed_common(bc_shape s, const bc_half* q, const bc_half* kv,
@@ -505,22 +632,17 @@ static int packed_common(bc_shape s, const bc_half* q, const bc_half* kv,
   P.max_pages = s.max_pages;
   P.phys_pages = s.physical_pages;
   P.scale_log2 = (float)((double)scale * 1.4426950408889634);
-  int chunk_tokens = 0, max_chunks = 1;
-  const size_t need = packed_workspace(s, &chunk_tokens, &max_chunks);
-  if (ws && need > 0 && ws_bytes >= need) {
-    P.splits = 0;
-    P.chunk_tokens = chunk_tokens;
-    P.max_chunks = max_chunks;
-    size_t acc_bytes = (size_t)s.batch * s.query_heads * max_chunks * s.dim *
-                       sizeof(float);
-    acc_bytes = (acc_bytes + 255) & ~(size_t)255;
+  const int nwg = packed_nwg(s);
+  const size_t need = packed_workspace(s, nwg);
+  if (ws && ws_bytes >= need) {
+    P.nwg = nwg;
+    const size_t slots = (size_t)nwg + s.batch;
+    const size_t acc_bytes =
+        (slots * s.query_heads * s.dim * sizeof(float) + 255) & ~(size_t)255;
     P.part_acc = static_cast<float*>(ws);
     P.part_ml = reinterpret_cast<float*>(static_cast<char*>(ws) + acc_bytes);
-    return launch<_Float16>(P, s.dim, max_chunks,
-                            reinterpret_cast<hipStream_t>(stream));
   }
-  P.splits = 1;
-  return launch<_Float16>(P, s.dim, 1, reinterpret_cast<hipStream_t>(stream));
+  return launch<_Float16>(P, s.dim, reinterpret_cast<hipStream_t>(stream));
 }
 
 extern "C" int bc_packed_decode(bc_shape s, const bc_half* q,

@@ -134,24 +134,28 @@ def test_packed_rejects(strides, scale):
 
 
 def test_auto_splits_policy():
+    """Split decode runs (splits - 1) * batch + 1 flat page ranges; the
+    heuristic picks the most that fit one 8-wave workgroup per CU."""
     lib = capi.load()
-    # contexts below 512 tokens stay unsplit (src/paged_gqa.cu:211)
-    assert lib.bc_auto_splits(_shape(batch=1), 511, 256) == 1
-    # long context, low batch: many splits, at least 128 tokens each, powers of 2
-    s4 = lib.bc_auto_splits(_shape(batch=4), 32768, 256)
-    assert s4 >= 16 and s4 & (s4 - 1) == 0 and 32768 // s4 >= 128
-    # large batches need no split to fill 256 CUs
+    assert lib.bc_auto_splits(_shape(batch=1), 63, 256) == 1  # tiny contexts stay whole
+    for batch in (1, 4, 16, 64, 200):
+        s = lib.bc_auto_splits(_shape(batch=batch), 32768, 256)
+        assert 1 <= s <= capi.BC_MAX_SPLITS
+        assert (s - 1) * batch + 1 <= 256
+        if s < capi.BC_MAX_SPLITS:
+            assert s * batch + 1 > 256  # one more split would overflow the CUs
+    assert lib.bc_auto_splits(_shape(batch=4), 32768, 256) == 64
     assert lib.bc_auto_splits(_shape(batch=512), 4096, 256) == 1
-    for ctx in (512, 1000, 4096, 100000):
-        s = lib.bc_auto_splits(_shape(batch=1), ctx, 256)
-        assert 1 <= s <= capi.BC_MAX_SPLITS and ctx // s >= 128
+    # more than eight head blocks per sequence: two workgroups per range
+    assert lib.bc_auto_splits(_shape(batch=1, query_heads=16, kv_heads=16), 4096, 256) == 128
 
 
 def test_workspace_sizes():
     lib = capi.load()
     c5 = capi.Shape(64, 32, 8, 128, 256, 20000)
     assert lib.bc_packed_decode_workspace_size(c5) > 0
-    assert lib.bc_packed_decode_workspace_size(capi.Shape(4, 32, 8, 128, 8, 64)) == 0
+    # flat page ranges are used whatever the context length
+    assert lib.bc_packed_decode_workspace_size(capi.Shape(4, 32, 8, 128, 8, 64)) > 0
     assert lib.bc_packed_decode_workspace_size(capi.Shape(4, 32, 8, 96, 8, 64)) == 0
     c3 = capi.Shape(8, 32, 8, 128, 129, 160)
     assert lib.bc_tree_verify_workspace_size(c3, 7) > 0
