@@ -48,6 +48,9 @@ def parse():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--only", default="", help="comma list of configs to run (c1..c5)")
+    ap.add_argument("--calibrate", action="store_true",
+                    help="also run a plain 512 MiB device copy, the known-size reference "
+                         "for scaling FETCH_SIZE / WRITE_SIZE counters")
     return ap.parse_args()
 
 
@@ -468,6 +471,16 @@ def main():
 
     def want(name):
         return not only or name in only
+
+    if args.calibrate:
+        src = torch.empty(256 * 1024 * 1024, device="cuda", dtype=torch.float16).fill_(1.0)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print("[bench] calibration copy: 5 x 512 MiB read + 512 MiB written",
+              file=sys.stderr, flush=True)
+        del src, dst
 
     c5 = C5(cx)
     call = c5.call(cx, workspace=True)
