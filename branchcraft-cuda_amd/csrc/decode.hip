@@ -446,12 +446,24 @@ __global__ __launch_bounds__(256) void merge_kernel(AttnParams P) {
 #pragma unroll
     for (int j = 0; j < PER; ++j) a[j] *= a1;
     mm = mn;
-    for (int i = 0; i < cnt; ++i) {
-      const float wi = __builtin_bit_cast(float, __builtin_amdgcn_readlane(
-                                                     __builtin_bit_cast(int, w), i));
-      const float* src = P.part_acc + ((size_t)(wb + i + b) * P.hq + h) * D + lane;
+    // Eight partials per step, all loads issued before the first use.  Parts
+    // past cnt re-read the last valid partial (finite) with weight 0.
+    for (int i0 = 0; i0 < cnt; i0 += 8) {
+      float v[8][PER];
 #pragma unroll
-      for (int j = 0; j < PER; ++j) a[j] += wi * src[64 * j];
+      for (int u = 0; u < 8; ++u) {
+        const int i = min(i0 + u, cnt - 1);
+        const float* src = P.part_acc + ((size_t)(wb + i + b) * P.hq + h) * D + lane;
+#pragma unroll
+        for (int j = 0; j < PER; ++j) v[u][j] = src[64 * j];
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const float wi = __builtin_bit_cast(
+            float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), min(i0 + u, 63)));
+#pragma unroll
+        for (int j = 0; j < PER; ++j) a[j] += wi * v[u][j];
+      }
     }
   }
   const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
