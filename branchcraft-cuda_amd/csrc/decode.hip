@@ -7,7 +7,7 @@
 // (src/packed_decode.cu:15-60).  The reference runs one 32-lane warp per
 // query head and walks tokens serially with a shuffle reduction per token.
 //
-// A workgroup holds one wave64 per KV head (up to eight) and walks a flat
+// A workgroup holds one wave64 per KV head (up to four) and walks a flat
 // range of pages, so the waves together stream every page as whole 16-slot
 // blocks.  The range is either one whole sequence or, for split decode, an
 // equal share of all the batch's pages: workgroup w of W takes pages
@@ -31,8 +31,8 @@
 // statistics (running max over raw scores, sum) use two cross-row lane
 // shuffles per page; scale*log2e is folded into the exp2 argument and the
 // output rescale is skipped unless a running max grows.  Page ids are scalar
-// loads fetched an iteration early, and each page's K/V loads are issued two
-// pages ahead of their use.
+// loads fetched an iteration early, and each page's K/V loads are issued while
+// the previous page is being processed.
 #include "bc_device.h"
 
 #include <math.h>
@@ -48,7 +48,9 @@ typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef short i16x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kMaxWaves = 8;
+// Four waves per workgroup at <= 168 VGPRs: up to three workgroups share a
+// CU, so a CU keeps 8-12 waves of page loads in flight.
+constexpr int kMaxWaves = 4;
 constexpr int kHeadCols = 16;  // MFMA N: query heads of one KV head per wave
 
 struct AttnParams {
@@ -171,7 +173,7 @@ __device__ __forceinline__ void wave_lds_sync() {
 }
 
 template <int D, typename OutT, bool VEC>
-__global__ __launch_bounds__(64 * kMaxWaves) void paged_attn_kernel(AttnParams P) {
+__global__ __launch_bounds__(64 * kMaxWaves, 3) void paged_attn_kernel(AttnParams P) {
   constexpr int KS = D / 32;  // QK k-steps
   constexpr int DT = D / 16;  // 16-dim output tiles
   constexpr int VP = D + 16;  // halves per staged V row
@@ -538,7 +540,7 @@ int device_cus() {
 
 // Flat-mode workgroup count for a given number of partial slots per head:
 // slot = workgroup + sequence must stay below `slots`, and a whole number of
-// waves of workgroups over the CUs (one 8-wave workgroup per CU) balances best.
+// waves of workgroups over the CUs balances best.
 int flat_workgroups(int batch, long long slots, int cus, int zgroups) {
   long long nwg = slots - batch + 1;
   const long long per_wave = cus / (zgroups > 0 ? zgroups : 1);
@@ -554,10 +556,10 @@ int zgroups_of(const bc_shape& s) {
   return (zdim + waves - 1) / waves;
 }
 
-// Packed decode with a workspace: flat ranges over one workgroup per CU.
+// Packed decode with a workspace: flat ranges over two workgroups per CU.
 int packed_nwg(const bc_shape& s) {
   const int zg = zgroups_of(s);
-  int n = device_cus() / zg;
+  int n = 2 * device_cus() / zg;
   return n < 1 ? 1 : n;
 }
 
@@ -604,7 +606,7 @@ extern "C" int bc_decode(bc_shape s, bc_inputs in, bc_scratch scratch,
 extern "C" int bc_auto_splits(bc_shape s, int max_length, int cu_count) {
   // Split decode runs flat page ranges: (splits - 1) * batch + 1 workgroups
   // share all pages equally.  Pick the largest split count whose workgroups
-  // fit one per CU; contexts under 64 tokens stay in one workgroup.
+  // fit one workgroup per CU; contexts under 64 tokens stay in one workgroup.
   if (max_length < 64 || s.batch < 1 || s.kv_heads < 1 || s.query_heads < 1 ||
       s.query_heads % s.kv_heads)
     return 1;

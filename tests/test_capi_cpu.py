@@ -134,20 +134,22 @@ def test_packed_rejects(strides, scale):
 
 
 def test_auto_splits_policy():
-    """Split decode runs (splits - 1) * batch + 1 flat page ranges; the
-    heuristic picks the most that fit one 8-wave workgroup per CU."""
+    """Split decode runs (splits - 1) * batch + 1 flat page ranges, each
+    served by ceil(kv head blocks / 4) four-wave workgroups; the heuristic
+    picks the most ranges whose workgroups fit one per CU."""
     lib = capi.load()
     assert lib.bc_auto_splits(_shape(batch=1), 63, 256) == 1  # tiny contexts stay whole
+    ranges = 256 // 2  # 8 KV heads: two four-wave workgroups per range
     for batch in (1, 4, 16, 64, 200):
         s = lib.bc_auto_splits(_shape(batch=batch), 32768, 256)
         assert 1 <= s <= capi.BC_MAX_SPLITS
-        assert (s - 1) * batch + 1 <= 256
+        assert (s - 1) * batch + 1 <= ranges
         if s < capi.BC_MAX_SPLITS:
-            assert s * batch + 1 > 256  # one more split would overflow the CUs
-    assert lib.bc_auto_splits(_shape(batch=4), 32768, 256) == 64
+            assert s * batch + 1 > ranges  # one more split would overflow the CUs
+    assert lib.bc_auto_splits(_shape(batch=4), 32768, 256) == 32
     assert lib.bc_auto_splits(_shape(batch=512), 4096, 256) == 1
-    # more than eight head blocks per sequence: two workgroups per range
-    assert lib.bc_auto_splits(_shape(batch=1, query_heads=16, kv_heads=16), 4096, 256) == 128
+    # sixteen KV heads: four workgroups per range
+    assert lib.bc_auto_splits(_shape(batch=1, query_heads=16, kv_heads=16), 4096, 256) == 64
 
 
 def test_workspace_sizes():
