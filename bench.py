@@ -37,6 +37,10 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT / "branchcraft-cuda_amd" / "python"))
 
 HBM_PEAK_GBS = 8000.0
+# HBM bytes per config-5 call measured with rocprofv3 counters: attention
+# FETCH 264,908.9 KiB x 2 + WRITE 5,029.6 KiB, merge FETCH 2,642.5 KiB x 2 +
+# WRITE 472.0 KiB (FETCH_SIZE reads half of a 512 MiB copy's bytes).
+C5_HBM_TRAFFIC_BYTES = (264908.9 * 2 + 5029.6 + 2642.5 * 2 + 472.0) * 1024
 MFMA_F16_PEAK_TFLOPS = 2500.0
 PAGE = 16
 
@@ -551,8 +555,12 @@ def main():
         },
         "roofline": {
             "bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
-            "kernel": "paged_attn_kernel<128,4,_Float16,true> + merge_kernel (one call)",
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": C5_HBM_TRAFFIC_BYTES,
+            "traffic_source": "rocprofv3 FETCH_SIZE (x2) + WRITE_SIZE (x1) per call, scaled "
+                              "by a 512 MiB copy; profiles/packed_decode_c5_hbm_traffic.md",
+            "kernel": ("paged_attn_kernel<128,_Float16,true> + merge_kernel<128,_Float16> "
+                       "(one bc_packed_decode_ws call; achieved = algorithmic bytes / "
+                       "HIP-event time per call on the launch stream)"),
             "algorithmic_bytes_per_launch": c5.bytes,
         },
         "cpu_baseline": cpu,
