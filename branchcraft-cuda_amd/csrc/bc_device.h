@@ -109,4 +109,12 @@ __device__ __forceinline__ uint4 ldg16(const uint16_t* p) {
   return *reinterpret_cast<const uint4*>(p);
 }
 
+// 16-byte load marked non-temporal (streaming): for data read once per call,
+// such as a decode's K/V pages, so they do not displace reused lines in L2.
+__device__ __forceinline__ uint4 ldg16_stream(const uint16_t* p) {
+  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+  const u32x4 w = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+  return make_uint4(w.x, w.y, w.z, w.w);
+}
+
 }  // namespace bcd

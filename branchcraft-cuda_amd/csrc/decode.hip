@@ -19,15 +19,18 @@
 // query heads of one KV head (the GQA group, up to 16) form MFMA tiles:
 //
 //   S^T[16 tok x 16 heads] = K[16 tok x D] . Q^T[D x 16 heads]
-//       (D/32 x v_mfma_f32_16x16x32_f16; lane = (token, 8-dim slice), so K
-//        feeds the A operand with one contiguous 16-byte load per k-step)
+//       (D/32 x v_mfma_f32_16x16x32_f16; A operand lane = (token, 8-dim slice))
 //   O^T[D x 16 heads]     += V^T[D x 16 tok] . P^T[16 tok x 16 heads]
 //       (D/16 x v_mfma_f32_16x16x16_f16 for P's FP16 hi part and again for
 //        its lo part, so P keeps ~22 bits; the S^T accumulator is already the
 //        P^T B operand, lane for lane)
 //
-// V is staged row-major in LDS (one 16-byte store per lane and k-step) and
-// the V^T A operand is read with ds_read_b64_tr_b16.  The per-head softmax
+// Pages are fetched as whole token rows (each 16-byte load instruction covers
+// complete 128-byte lines) with non-temporal loads: K/V are read once per
+// call, and full-line streaming loads run at ~7 TB/s on MI355X where
+// partial-line or cached loads stay near 6.  Both K and V are staged
+// row-major in LDS: K is read back in the A-operand layout (ds_read_b128),
+// V^T through ds_read_b64_tr_b16.  The per-head softmax
 // statistics (running max over raw scores, sum) use two cross-row lane
 // shuffles per page; scale*log2e is folded into the exp2 argument and the
 // output rescale is skipped unless a running max grows.  Page ids are scalar
@@ -151,9 +154,10 @@ __device__ __forceinline__ void store_out(void* out, size_t idx, float x) {
 
 // Eight consecutive FP16 values; VEC selects one 16-byte load, otherwise
 // eight 2-byte loads (for strides or bases that are not 8-element aligned).
-template <bool VEC>
+// STREAM marks the 16-byte load non-temporal (K/V pages are read once).
+template <bool VEC, bool STREAM = false>
 __device__ __forceinline__ uint4 load8(const uint16_t* p) {
-  if (VEC) return ldg16(p);
+  if (VEC) return STREAM ? ldg16_stream(p) : ldg16(p);
   uint32_t w[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) w[i] = (uint32_t)p[2 * i] | ((uint32_t)p[2 * i + 1] << 16);
@@ -174,10 +178,15 @@ __device__ __forceinline__ void wave_lds_sync() {
 
 template <int D, typename OutT, bool VEC>
 __global__ __launch_bounds__(64 * kMaxWaves, 3) void paged_attn_kernel(AttnParams P) {
-  constexpr int KS = D / 32;  // QK k-steps
-  constexpr int DT = D / 16;  // 16-dim output tiles
-  constexpr int VP = D + 16;  // halves per staged V row
+  constexpr int KS = D / 32;   // QK k-steps (and 16-byte loads per page row set)
+  constexpr int DT = D / 16;   // 16-dim output tiles
+  constexpr int VP = D + 16;   // halves per staged V row
+  constexpr int KP = D + 8;    // halves per staged K row
+  constexpr int LPR = D / 8;   // lanes per token row in a page load
+  constexpr int RPI = 64 / LPR;  // token rows per load instruction
+  static_assert(RPI * KS == BC_PAGE_SIZE, "one page = KS loads per lane");
   __shared__ __attribute__((aligned(16))) _Float16 s_v[kMaxWaves * 16 * VP];
+  __shared__ __attribute__((aligned(16))) _Float16 s_k[kMaxWaves * 16 * KP];
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -268,10 +277,16 @@ __global__ __launch_bounds__(64 * kMaxWaves, 3) void paged_attn_kernel(AttnParam
   };
 
   _Float16* vs = s_v + wave * 16 * VP;
+  _Float16* ks = s_k + wave * 16 * KP;
   // Transpose-read address: lane (g4, c16) names [token 4*g4 + c16/4][4*(c16%4)].
   const _Float16* vtr = vs + (4 * g4 + (c16 >> 2)) * VP + 4 * (c16 & 3);
+  // Page loads read whole token rows: load s of a lane covers token
+  // s*RPI + lane/LPR, dims 8*(lane%LPR) .. +8, so every instruction fetches
+  // complete 128-byte lines (streaming loads then stay at full rate).
+  const int lrow = lane / LPR, lcol = 8 * (lane % LPR);
   const long long lane_off =
-      (long long)kvh * P.head_stride + (long long)c16 * P.slot_stride + 8 * g4;
+      (long long)kvh * P.head_stride + (long long)lrow * P.slot_stride + lcol;
+  const long long row_step = (long long)RPI * P.slot_stride;
 
   // Issue cursor: walks the same pages ahead of the compute cursor.  Page
   // ids are scalar loads (counted by lgkmcnt, not vmcnt), fetched one step
@@ -296,9 +311,9 @@ __global__ __launch_bounds__(64 * kMaxWaves, 3) void paged_attn_kernel(AttnParam
     valid = phys >= 0 && phys < P.phys_pages;
     const long long base = (valid ? (long long)phys : 0ll) * P.page_stride + lane_off;
 #pragma unroll
-    for (int s = 0; s < KS; ++s) kb[s] = load8<VEC>(P.kbase + base + 32 * s);
+    for (int s = 0; s < KS; ++s) kb[s] = load8<VEC, true>(P.kbase + base + s * row_step);
 #pragma unroll
-    for (int s = 0; s < KS; ++s) vb[s] = load8<VEC>(P.vbase + base + 32 * s);
+    for (int s = 0; s < KS; ++s) vb[s] = load8<VEC, true>(P.vbase + base + s * row_step);
   };
 
   auto process = [&](int idx, const uint4 (&kb)[KS], uint4 (&vb)[KS], bool valid) {
@@ -308,21 +323,26 @@ __global__ __launch_bounds__(64 * kMaxWaves, 3) void paged_attn_kernel(AttnParam
     if (!full) {
       // Slots past the length may hold any bits (NaN included); their weight
       // is zero, so their V row must be zero too.
-      if (!(valid && t0 + c16 < plen)) {
 #pragma unroll
-        for (int s = 0; s < KS; ++s) vb[s] = make_uint4(0, 0, 0, 0);
-      }
+      for (int s = 0; s < KS; ++s)
+        if (!(valid && t0 + s * RPI + lrow < plen)) vb[s] = make_uint4(0, 0, 0, 0);
     }
+    // Stage the page's K and V rows; K comes back in the A-operand layout
+    // (lane = token c16, dims 32s + 8*g4), V through transpose reads.
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      *reinterpret_cast<uint4*>(ks + (s * RPI + lrow) * KP + lcol) = kb[s];
+      *reinterpret_cast<uint4*>(vs + (s * RPI + lrow) * VP + lcol) = vb[s];
+    }
+    wave_lds_sync();
     f32x4 sc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int s = 0; s < KS; ++s)
-      sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, kb[s]),
+    for (int s = 0; s < KS; ++s) {
+      const uint4 ka = *reinterpret_cast<const uint4*>(ks + c16 * KP + 32 * s + 8 * g4);
+      sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, ka),
                                                  __builtin_bit_cast(f16x8, qB[s]),
                                                  sc, 0, 0, 0);
-    // Stage V while the MFMAs drain.
-#pragma unroll
-    for (int s = 0; s < KS; ++s)
-      *reinterpret_cast<uint4*>(vs + c16 * VP + 32 * s + 8 * g4) = vb[s];
+    }
 
     float sv[4];
 #pragma unroll
@@ -348,7 +368,6 @@ __global__ __launch_bounds__(64 * kMaxWaves, 3) void paged_attn_kernel(AttnParam
       ph[j] = (_Float16)pr;
       pl[j] = (_Float16)(pr - (float)ph[j]);
     }
-    wave_lds_sync();
 #pragma unroll
     for (int t = 0; t < DT; ++t) {
       const f16x4 a = lds_read_tr(vtr + 16 * t);
