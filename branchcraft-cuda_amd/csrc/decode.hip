@@ -37,10 +37,9 @@
 // loads fetched an iteration early, and each page's K/V loads are issued while
 // the previous page is being processed.
 #include "bc_device.h"
+#include "bc_host.h"
 
 #include <math.h>
-
-#include <atomic>
 
 namespace {
 
@@ -539,23 +538,7 @@ hipError_t launch(AttnParams& P, int dim, hipStream_t st) {
                    : launch_dim<128, OutT>(P, vec, st);
 }
 
-// Compute units of the current device (cached per device; an immutable
-// attribute, so the cache is safe to share between threads).
-int device_cus() {
-  static std::atomic<int> cache[64];
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 256;
-  if (dev < 64) {
-    const int v = cache[dev].load(std::memory_order_relaxed);
-    if (v > 0) return v;
-  }
-  int n = 0;
-  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-      n < 1)
-    n = 256;
-  if (dev < 64) cache[dev].store(n, std::memory_order_relaxed);
-  return n;
-}
+using bch::device_cus;
 
 // Flat-mode workgroup count for a given number of partial slots per head:
 // slot = workgroup + sequence must stay below `slots`, and a whole number of

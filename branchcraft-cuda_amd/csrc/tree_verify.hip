@@ -32,6 +32,7 @@
 // combines.  Workgroup ids put (KV head, row tile) in the low bits, so the
 // requests that share prefix pages run on the same XCD and reuse its L2.
 #include "bc_device.h"
+#include "bc_host.h"
 
 namespace {
 
@@ -103,6 +104,18 @@ __global__ __launch_bounds__(kThreads) void tree_kernel(TreeParams P) {
   const int kvh = z / P.row_tiles;
   const int rt = z % P.row_tiles;
 
+  // Page ids of this wave's first prefix tile, requested together with the
+  // length (they do not depend on it) so the first K/V loads wait for one
+  // memory round trip instead of two.
+  int ida[2];
+  {
+    const int tp0s = P.part_acc && part < P.prefix_parts ? part * P.chunk_tokens / kTile : 0;
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int pg = (tp0s + wave) * (kTile / BC_PAGE_SIZE) + q;
+      ida[q] = pg < P.max_pages ? P.pages[(size_t)b * P.max_pages + pg] : -1;
+    }
+  }
   const int len = max(0, min(P.lengths[b], P.max_pages * BC_PAGE_SIZE));
   int pbeg = 0, pend = len;
   bool drafts = true, final_out = true;
@@ -155,46 +168,89 @@ __global__ __launch_bounds__(kThreads) void tree_kernel(TreeParams P) {
   float m = kNegInf, l = 0.f;
 
   const size_t tok_stride = (size_t)P.hkv * D;  // elements between slots
+  const int ntile = ntile_p + ntile_d;
+  const int nmine = ntile > wave ? (ntile - wave + kWaves - 1) / kWaves : 0;
 
-  for (int it = wave; it < ntile_p + ntile_d; it += kWaves) {
-    const bool is_draft = it >= ntile_p;
-    // ---- load this lane's token row (token lr of the tile) ----
+  // Tile `idx` of this wave is tile wave + kWaves*idx of the workgroup.  The
+  // loads of a tile are issued one tile ahead of its MFMAs; issues past the
+  // wave's last tile repeat that tile (L2 hits), so every iteration has the
+  // same loads in flight and the loop body never exits early.
+  auto tile_of = [&](int idx) { return wave + kWaves * min(idx, max(nmine - 1, 0)); };
+  // Physical ids of a prefix tile's two pages: uniform scalar loads, fetched
+  // one tile before the K/V loads that use them.
+  auto ids_of = [&](int idx, int (&ph)[2]) {
+    const int it = tile_of(idx);
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int pg = (tp0 + it) * (kTile / BC_PAGE_SIZE) + q;
+      ph[q] = it < ntile_p && pg < P.max_pages ? P.pages[(size_t)b * P.max_pages + pg] : -1;
+    }
+  };
+  auto issue = [&](int idx, const int (&ph)[2], uint4 (&kr)[KS], uint4 (&vr)[KS], bool& tv,
+                   bool (&pok)[2]) {
+    const int it = tile_of(idx);
     const uint16_t* kp;
     const uint16_t* vp;
-    bool tv;
-    int tbase;          // first token (prefix) or first node (draft) of tile
-    bool page_ok[2] = {true, true};
-    if (!is_draft) {
-      tbase = (tp0 + it) * kTile;
-      // The two pages of the tile (uniform scalar loads).
+    if (it < ntile_p) {
+      const int tbase = (tp0 + it) * kTile;
 #pragma unroll
-      for (int q = 0; q < 2; ++q) {
-        const int pg = tbase / BC_PAGE_SIZE + q;
-        const int phys = pg < P.max_pages ? P.pages[(size_t)b * P.max_pages + pg] : -1;
-        page_ok[q] = phys >= 0 && phys < P.phys_pages;
-      }
+      for (int q = 0; q < 2; ++q) pok[q] = ph[q] >= 0 && ph[q] < P.phys_pages;
       const int t = tbase + lr;
-      tv = t >= pbeg && t < pend && page_ok[lr >> 4];
-      size_t off = 0;
-      if (tv) {
-        const size_t phys = (size_t)P.pages[(size_t)b * P.max_pages + t / BC_PAGE_SIZE];
-        off = (phys * BC_PAGE_SIZE + t % BC_PAGE_SIZE) * tok_stride + (size_t)kvh * D;
-      }
+      tv = t >= pbeg && t < pend && pok[lr >> 4];
+      const size_t phys = (size_t)(tv ? (lr >> 4 ? ph[1] : ph[0]) : 0);
+      const size_t off =
+          tv ? (phys * BC_PAGE_SIZE + t % BC_PAGE_SIZE) * tok_stride + (size_t)kvh * D : 0;
       kp = P.k + off;
       vp = P.v + off;
     } else {
-      tbase = (it - ntile_p) * kTile;
-      const int dn = tbase + lr;
+      pok[0] = pok[1] = true;
+      const int dn = (it - ntile_p) * kTile + lr;
       tv = dn < P.nodes;
       const size_t off = tv ? (((size_t)b * P.nodes + dn) * P.hkv + kvh) * D : 0;
       kp = P.dk + off;
       vp = P.dv + off;
     }
-    uint4 kreg[KS], vreg[KS];
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
-      kreg[s] = tv ? ldg16(kp + 16 * s + 8 * g) : make_uint4(0, 0, 0, 0);
-      vreg[s] = tv ? ldg16(vp + 16 * s + 8 * g) : make_uint4(0, 0, 0, 0);
+      kr[s] = ldg16(kp + 16 * s + 8 * g);
+      vr[s] = ldg16(vp + 16 * s + 8 * g);
+    }
+  };
+
+  auto process = [&](int idx, const uint4 (&kr)[KS], uint4 (&vr)[KS], bool tv,
+                     const bool (&pok)[2]) {
+    if (idx >= nmine) return;  // padding step
+    const int it = wave + kWaves * idx;
+    const bool is_draft = it >= ntile_p;
+    const int tbase = is_draft ? (it - ntile_p) * kTile : (tp0 + it) * kTile;
+    // Valid token rows of the tile as a bit mask (bit i = token tbase + i):
+    // prefix tiles clip [pbeg, pend) and drop pages outside the pool (uniform
+    // over the wave); draft tiles take this row's ancestor-or-self set.
+    uint32_t okbits;
+    if (!is_draft) {
+      const int lo = min(max(pbeg - tbase, 0), kTile);
+      const int hi = min(max(pend - tbase, 0), kTile);
+      const uint32_t below_hi = hi >= kTile ? ~0u : (1u << hi) - 1u;
+      const uint32_t below_lo = lo >= kTile ? ~0u : (1u << lo) - 1u;
+      okbits = (below_hi & ~below_lo) & ((pok[0] ? 0x0000ffffu : 0u) | (pok[1] ? 0xffff0000u : 0u));
+    } else {
+      okbits = 0;
+      int cur = node;
+      for (int steps = 0; steps < P.nodes && cur >= 0 && cur < P.nodes; ++steps) {
+        if (cur >= tbase && cur < tbase + kTile) okbits |= 1u << (cur - tbase);
+        cur = s_parent[cur];
+      }
+    }
+    // Rows past the prefix or the node count may hold any bits (NaN
+    // included); their weight is zero, so their V row must be zero too.
+    if (is_draft || okbits != ~0u) {
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        vr[s].x = tv ? vr[s].x : 0u;
+        vr[s].y = tv ? vr[s].y : 0u;
+        vr[s].z = tv ? vr[s].z : 0u;
+        vr[s].w = tv ? vr[s].w : 0u;
+      }
     }
 
     // ---- S^T = K Q^T ----
@@ -203,36 +259,22 @@ __global__ __launch_bounds__(kThreads) void tree_kernel(TreeParams P) {
     for (int j = 0; j < 16; ++j) sc[j] = 0.f;
 #pragma unroll
     for (int s = 0; s < KS; ++s)
-      sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_f16x8(kreg[s]),
+      sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_f16x8(kr[s]),
                                                   as_f16x8(qreg[s]), sc, 0, 0, 0);
 
     // ---- stage V row-major while the MFMAs drain ----
 #pragma unroll
     for (int s = 0; s < KS; ++s)
-      *reinterpret_cast<uint4*>(vs + lr * VP + 16 * s + 8 * g) = vreg[s];
+      *reinterpret_cast<uint4*>(vs + lr * VP + 16 * s + 8 * g) = vr[s];
 
     // ---- mask and online softmax (column lr = query row) ----
-    uint32_t anc = 0;
-    if (is_draft) {
-      // Ancestor-or-self bits of this row's node inside draft tile tbase.
-      int cur = node;
-      for (int steps = 0; steps < P.nodes && cur >= 0 && cur < P.nodes; ++steps) {
-        if (cur >= tbase && cur < tbase + kTile) anc |= 1u << (cur - tbase);
-        cur = s_parent[cur];
-      }
-    }
+    // sc[j] holds token row 8*(j/4) + 4*g + j%4.
+    const uint32_t ob = okbits >> (4 * g);
     float sv[16];
     float tmax = kNegInf;
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
-      const int tk = 8 * (j >> 2) + 4 * g + (j & 3);  // token row of sc[j]
-      bool ok;
-      if (is_draft) {
-        ok = (anc >> tk) & 1u;
-      } else {
-        const int t = tbase + tk;
-        ok = t >= pbeg && t < pend && page_ok[tk >> 4];
-      }
+      const bool ok = (ob >> (8 * (j >> 2) + (j & 3))) & 1u;
       sv[j] = ok ? sc[j] * P.scale_log2 : kNegInf;
       tmax = __builtin_fmaxf(tmax, sv[j]);
     }
@@ -278,16 +320,35 @@ __global__ __launch_bounds__(kThreads) void tree_kernel(TreeParams P) {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  }
+  };
 
+  uint4 ka[KS], va[KS], kb[KS], vb[KS];
+  bool ta = false, tb = false;
+  bool pa[2] = {true, true}, pbk[2] = {true, true};
+  int idb[2];
+  if (nmine > 0) {
+    issue(0, ida, ka, va, ta, pa);
+    ids_of(1, idb);
+    for (int idx = 0; idx < nmine; idx += 2) {
+      issue(idx + 1, idb, kb, vb, tb, pbk);
+      ids_of(idx + 2, ida);
+      process(idx, ka, va, ta, pa);
+      issue(idx + 2, ida, ka, va, ta, pa);
+      ids_of(idx + 3, idb);
+      process(idx + 1, kb, vb, tb, pbk);
+    }
+  }
   // Both lane halves share m; combine their partial sums.
   l += shfl_xor_f(l, 32);
 
   // ---- merge the four waves: 3,2 -> 1,0 then 1 -> 0 through LDS ----
-  static_assert(kWaves * kTile * VP * 2 >= 2 * 32 * D * 4, "merge buffer fits");
-  float* xacc = reinterpret_cast<float*>(s_mem);  // [2][32 rows][D]
+  // Rows are padded to D + 4 floats so the 32 rows a float4 access touches
+  // fall in different LDS banks.
+  constexpr int XP = D + 4;
+  static_assert(kWaves * kTile * VP * 2 >= 2 * 32 * XP * 4, "merge buffer fits");
+  float* xacc = reinterpret_cast<float*>(s_mem);  // [2][32 rows][XP]
   auto put = [&](int slot) {
-    float* dst = xacc + (size_t)slot * 32 * D + (size_t)lr * D;
+    float* dst = xacc + (size_t)slot * 32 * XP + (size_t)lr * XP;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
@@ -302,7 +363,7 @@ __global__ __launch_bounds__(kThreads) void tree_kernel(TreeParams P) {
     }
   };
   auto take = [&](int slot) {
-    const float* src = xacc + (size_t)slot * 32 * D + (size_t)lr * D;
+    const float* src = xacc + (size_t)slot * 32 * XP + (size_t)lr * XP;
     const float m2 = s_m[slot][lr], l2 = s_l[slot][lr];
     const float mm = __builtin_fmaxf(m, m2);
     const float a1 = fast_exp2(m - safe_max(mm)), a2 = fast_exp2(m2 - safe_max(mm));
@@ -390,12 +451,23 @@ __global__ __launch_bounds__(256) void merge_tree_kernel(TreeParams P) {
   float a[PER];
 #pragma unroll
   for (int j = 0; j < PER; ++j) a[j] = 0.f;
-  for (int i = 0; i <= nparts; ++i) {
-    const float wi = __builtin_bit_cast(float, __builtin_amdgcn_readlane(
-                                                   __builtin_bit_cast(int, w), i));
-    const float* src = P.part_acc + slot(i) * D + lane;
+  // Eight parts per step, all loads issued before the first use; steps past
+  // the last part re-read it with weight 0 (lanes past nparts hold w = 0).
+  for (int i0 = 0; i0 <= nparts; i0 += 8) {
+    float v[8][PER];
 #pragma unroll
-    for (int j = 0; j < PER; ++j) a[j] += wi * src[64 * j];
+    for (int u = 0; u < 8; ++u) {
+      const float* src = P.part_acc + slot(min(i0 + u, nparts)) * D + lane;
+#pragma unroll
+      for (int j = 0; j < PER; ++j) v[u][j] = src[64 * j];
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const float wi = __builtin_bit_cast(
+          float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), min(i0 + u, 63)));
+#pragma unroll
+      for (int j = 0; j < PER; ++j) a[j] += wi * v[u][j];
+    }
   }
   const float inv = 1.f / lsum;
 #pragma unroll
@@ -440,14 +512,15 @@ TreeParams make_params(const bc_shape& s, const bc_tree_inputs& in, int nodes) {
   return P;
 }
 
-// Prefix chunking for the workspace path: enough workgroups to cover the
-// 256 CUs about twice, chunks of at least 128 tokens, multiples of 32.
+// Prefix chunking for the workspace path: one workgroup per CU (the kernel
+// fits one per CU), counting the draft part of every unit, chunks of at
+// least 128 tokens, multiples of 32.
 void tree_chunking(const bc_shape& s, int nodes, int* chunk_tokens, int* parts) {
   const int group = s.query_heads / s.kv_heads;
   const long long units =
       (long long)s.batch * s.kv_heads * ((nodes * group + 31) / 32);
   const int max_tokens = s.max_pages * BC_PAGE_SIZE;
-  long long want = (512 + units - 1) / units;
+  long long want = bch::device_cus() / units - 1;
   if (want < 1) want = 1;
   int chunk = (int)((max_tokens + want - 1) / want);
   chunk = (chunk + kTile - 1) / kTile * kTile;
