@@ -1,6 +1,5 @@
-// Device helpers shared by the Branchcraft gfx950 kernels: FP16 packing,
-// packed-FP16 dot products, DPP reductions inside wave64 lane groups and a
-// base-2 online-softmax state.
+// Device helpers shared by the Branchcraft gfx950 kernels: exp2, DPP and
+// cross-row reductions over wave64 lanes, and 16-byte loads.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -10,34 +9,8 @@
 
 namespace bcd {
 
-typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
-
 constexpr float kNegInf = -__builtin_huge_valf();
 constexpr float kLog2e = 1.4426950408889634f;
-
-__device__ __forceinline__ f16x2 as_f16x2(uint32_t u) {
-  return __builtin_bit_cast(f16x2, u);
-}
-
-// 8-element FP16 dot product, FP32 accumulate (v_dot2_f32_f16 x4).
-__device__ __forceinline__ float dot8(const uint4 a, const uint4 b, float acc) {
-  acc = __builtin_amdgcn_fdot2(as_f16x2(a.x), as_f16x2(b.x), acc, false);
-  acc = __builtin_amdgcn_fdot2(as_f16x2(a.y), as_f16x2(b.y), acc, false);
-  acc = __builtin_amdgcn_fdot2(as_f16x2(a.z), as_f16x2(b.z), acc, false);
-  acc = __builtin_amdgcn_fdot2(as_f16x2(a.w), as_f16x2(b.w), acc, false);
-  return acc;
-}
-
-// acc[0..7] += p * v[0..7] with v packed FP16 (folds into v_fma_mix_f32).
-__device__ __forceinline__ void axpy8(float p, const uint4 v, float* acc) {
-  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const f16x2 h = as_f16x2(w[i]);
-    acc[2 * i] = __builtin_fmaf(p, (float)h.x, acc[2 * i]);
-    acc[2 * i + 1] = __builtin_fmaf(p, (float)h.y, acc[2 * i + 1]);
-  }
-}
 
 __device__ __forceinline__ float fast_exp2(float x) {
   return __builtin_amdgcn_exp2f(x);  // v_exp_f32; exp2(-inf) == 0
@@ -69,23 +42,6 @@ __device__ __forceinline__ float group_sum(float x) {
   return x;
 }
 
-// group_sum over N independent values, one DPP step at a time across all of
-// them, so consecutive DPP reads never depend on the instruction just before.
-template <int GROUP, int N>
-__device__ __forceinline__ void group_sum_n(float (&x)[N]) {
-  static_assert(GROUP == 8 || GROUP == 16, "group of 8 or 16 lanes");
-  if (GROUP == 16) {
-#pragma unroll
-    for (int i = 0; i < N; ++i) x[i] += dpp_f<kDppRowMirror>(x[i]);
-  }
-#pragma unroll
-  for (int i = 0; i < N; ++i) x[i] += dpp_f<kDppRowHalfMirror>(x[i]);
-#pragma unroll
-  for (int i = 0; i < N; ++i) x[i] += dpp_f<kDppQuadXor2>(x[i]);
-#pragma unroll
-  for (int i = 0; i < N; ++i) x[i] += dpp_f<kDppQuadXor1>(x[i]);
-}
-
 template <int GROUP>
 __device__ __forceinline__ float group_max(float x) {
   static_assert(GROUP == 8 || GROUP == 16, "group of 8 or 16 lanes");
@@ -98,6 +54,34 @@ __device__ __forceinline__ float group_max(float x) {
 
 __device__ __forceinline__ float shfl_xor_f(float x, int mask) {
   return __shfl_xor(x, mask, 64);
+}
+
+// Whole-wave reductions, every lane receiving the result: DPP inside each
+// 16-lane row (no LDS traffic), then two cross-row shuffles.
+__device__ __forceinline__ float wave_sum(float x) {
+  x = group_sum<16>(x);
+  x += shfl_xor_f(x, 16);
+  return x + shfl_xor_f(x, 32);
+}
+
+__device__ __forceinline__ float wave_max(float x) {
+  x = group_max<16>(x);
+  x = __builtin_fmaxf(x, shfl_xor_f(x, 16));
+  return __builtin_fmaxf(x, shfl_xor_f(x, 32));
+}
+
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int x) {
+  return __builtin_amdgcn_update_dpp(0, x, CTRL, 0xf, 0xf, false);
+}
+
+__device__ __forceinline__ int wave_sum_i(int x) {
+  x += dpp_i<kDppRowMirror>(x);
+  x += dpp_i<kDppRowHalfMirror>(x);
+  x += dpp_i<kDppQuadXor2>(x);
+  x += dpp_i<kDppQuadXor1>(x);
+  x += __shfl_xor(x, 16, 64);
+  return x + __shfl_xor(x, 32, 64);
 }
 
 // Exponent base used when folding a running max that may still be -inf.

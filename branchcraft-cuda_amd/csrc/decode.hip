@@ -83,12 +83,6 @@ __device__ __forceinline__ int seq_pages(const AttnParams& P, int b) {
   return (seq_len(P, b) + BC_PAGE_SIZE - 1) / BC_PAGE_SIZE;
 }
 
-__device__ __forceinline__ int wave_sum_i(int x) {
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) x += __shfl_xor(x, off, 64);
-  return x;
-}
-
 __device__ __forceinline__ int wave_incl_scan_i(int x, int lane) {
 #pragma unroll
   for (int off = 1; off < 64; off <<= 1) {
@@ -409,18 +403,6 @@ __global__ __launch_bounds__(64 * kMaxWaves, 3) void paged_attn_kernel(AttnParam
   }
   // The range ended inside sequence pb: leave a partial.
   if (plocal != ppages) finalize(false);
-}
-
-__device__ __forceinline__ float wave_max(float x) {
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) x = __builtin_fmaxf(x, shfl_xor_f(x, off));
-  return x;
-}
-
-__device__ __forceinline__ float wave_sum(float x) {
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) x += shfl_xor_f(x, off);
-  return x;
 }
 
 // Flat mode: out = sum_w 2^(m_w - M) a_w / sum_w 2^(m_w - M) l_w over the

@@ -441,13 +441,9 @@ __global__ __launch_bounds__(256) void merge_tree_kernel(TreeParams P) {
     mp = P.part_ml[2 * slot(lane)];
     lp = P.part_ml[2 * slot(lane) + 1];
   }
-  float mm = mp;
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) mm = __builtin_fmaxf(mm, shfl_xor_f(mm, off));
+  const float mm = wave_max(mp);
   const float w = fast_exp2(mp - mm);  // every row sees its own node: mm finite
-  float lsum = w * lp;
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) lsum += shfl_xor_f(lsum, off);
+  const float lsum = wave_sum(w * lp);
   float a[PER];
 #pragma unroll
   for (int j = 0; j < PER; ++j) a[j] = 0.f;
