@@ -86,3 +86,19 @@ def test_split_matches_single_at_scale():
     single = G.decode(q, k, v, pages, lengths, 1)
     for splits in (2, 16, 128):
         G.gate(G.decode(q, k, v, pages, lengths, splits), single, 3e-4, f"splits={splits}")
+
+
+@pytest.mark.parametrize("hq,hkv,d", [(8, 8, 128), (32, 1, 64), (64, 2, 128), (48, 3, 64),
+                                      (40, 8, 128), (24, 6, 64)])
+def test_head_layouts_beyond_reference(hq, hkv, d, oracle):
+    """Multi-head (group 1), one KV head for 32 query heads (two 16-column
+    head blocks per KV head), group 32 with two KV heads, and groups that
+    leave part of a head block empty (16, 5 and 4 heads), with and without
+    splits."""
+    rng = np.random.default_rng(hq * 131 + hkv * 7 + d)
+    lens = [0, 31, 200, 1029]
+    q, k, v, pages, lengths = oracle_np.paged_fixture(rng, len(lens), hq, hkv, d, lens)
+    expected = oracle.decode(q, k, v, pages, lengths, threads=8)
+    for splits in (1, 3, 40):
+        out = G.decode(q, k, v, pages, lengths, splits)
+        G.gate(out, expected, 3e-4, f"Hq={hq} Hkv={hkv} D={d} splits={splits}")

@@ -70,6 +70,16 @@ def test_wide_trees_span_row_and_draft_tiles(nodes, hq, hkv, oracle):
     _check(fix, oracle, atol=3e-4, what=f"N={nodes}")
 
 
+@pytest.mark.parametrize("hq,hkv,d,prefix", [(8, 8, 128, 300), (32, 1, 64, 129),
+                                             (48, 3, 64, 517), (20, 4, 128, 33)])
+def test_head_layouts_beyond_reference(hq, hkv, d, prefix, oracle):
+    """Group 1 (7 rows per KV head), group 32 (224 rows: seven row tiles),
+    group 16 and group 5 (35 rows: a second, mostly empty row tile)."""
+    rng = np.random.default_rng(hq + 13 * hkv + d + prefix)
+    fix = oracle_np.tree_fixture(rng, 3, prefix, 7, hq=hq, hkv=hkv, d=d, parents="random")
+    _check(fix, oracle, atol=3e-4, what=f"Hq={hq} Hkv={hkv} D={d}")
+
+
 def test_tree_equals_expanded_decode(oracle):
     rng = np.random.default_rng(91)
     k, v, pages, lengths, dq, dk, dv, par = oracle_np.tree_fixture(rng, 4, 300, 7,
