@@ -72,7 +72,8 @@ struct AttnParams {
   int waves;              // waves per workgroup (head blocks per workgroup)
   float scale_log2;       // softmax scale * log2(e)
   int nwg;                // > 0: flat page ranges over nwg workgroups;
-                          // 0: one workgroup per sequence
+                          // 0: one workgroup per (sequence, head block), its
+                          // waves splitting the pages (merged through LDS)
 };
 
 __device__ __forceinline__ int seq_len(const AttnParams& P, int b) {
@@ -178,8 +179,14 @@ __global__ __launch_bounds__(64 * kMaxWaves, 3) void paged_attn_kernel(AttnParam
   constexpr int LPR = D / 8;   // lanes per token row in a page load
   constexpr int RPI = 64 / LPR;  // token rows per load instruction
   static_assert(RPI * KS == BC_PAGE_SIZE, "one page = KS loads per lane");
-  __shared__ __attribute__((aligned(16))) _Float16 s_v[kMaxWaves * 16 * VP];
-  __shared__ __attribute__((aligned(16))) _Float16 s_k[kMaxWaves * 16 * KP];
+  // Per-wave K/V staging; reused after the page loop by the sliced mode's
+  // merge of [wave][head][D + 4] FP32 states.
+  constexpr int XP = D + 4;
+  constexpr size_t kStage = (size_t)kMaxWaves * 16 * (VP + KP) * 2;
+  constexpr size_t kMerge = (size_t)kMaxWaves * 16 * (XP + 2) * 4;
+  __shared__ __attribute__((aligned(16))) char s_mem[kStage > kMerge ? kStage : kMerge];
+  _Float16* const s_v = reinterpret_cast<_Float16*>(s_mem);
+  _Float16* const s_k = s_v + kMaxWaves * 16 * VP;
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -187,11 +194,14 @@ __global__ __launch_bounds__(64 * kMaxWaves, 3) void paged_attn_kernel(AttnParam
   const int c16 = lane & 15;  // token row of A, head column of B and C
 
   // blockIdx.x = range * zgroups + zg; wave -> head block z.
+  // Flat mode: blockIdx.x = range * zgroups + zg, wave -> head block z.
+  // Sliced mode (nwg == 0): blockIdx.x = sequence * zdim + z, every wave on
+  // head block z, wave w on the w-th quarter of the sequence's pages.
+  const bool sliced = P.nwg == 0;
   const int zgroups = (P.zdim + P.waves - 1) / P.waves;
-  const int zg = blockIdx.x % zgroups;
-  const int rid = blockIdx.x / zgroups;
-  const int z = zg * P.waves + wave;
-  if (z >= P.zdim) return;  // no workgroup barrier below
+  const int rid = sliced ? blockIdx.x / P.zdim : blockIdx.x / zgroups;
+  const int z = sliced ? blockIdx.x % P.zdim : (blockIdx.x % zgroups) * P.waves + wave;
+  if (z >= P.zdim) return;  // flat mode only: no workgroup barrier there
   const int kvh = z / P.nblk;
   const int h0 = kvh * P.group + (z % P.nblk) * kHeadCols;
   const int nh = min(kHeadCols, P.group - (z % P.nblk) * kHeadCols);
@@ -200,18 +210,11 @@ __global__ __launch_bounds__(64 * kMaxWaves, 3) void paged_attn_kernel(AttnParam
   // This workgroup's pages: sequence pb from local page `plocal`, `count`
   // pages in all (crossing into later sequences in flat mode).
   int pb, plocal, count;
-  if (P.nwg == 0) {
+  if (sliced) {
     pb = rid;
-    plocal = 0;
-    count = seq_pages(P, pb);
-    if (count == 0) {  // empty sequence: zeros (src/paged_gqa.cu:63)
-      if (c16 < nh) {
-        const size_t o = ((size_t)pb * P.hq + h0 + c16) * D + 4 * g4;
-#pragma unroll
-        for (int t = 0; t < DT; ++t) store4<OutT>(P.out, o + 16 * t, 0.f, 0.f, 0.f, 0.f);
-      }
-      return;
-    }
+    const int np = seq_pages(P, pb);
+    plocal = wave * np / P.waves;
+    count = (wave + 1) * np / P.waves - plocal;  // may be 0 (an empty slice)
   } else {
     int total, per;
     flat_geometry(P, lane, total, per);
@@ -371,7 +374,7 @@ __global__ __launch_bounds__(64 * kMaxWaves, 3) void paged_attn_kernel(AttnParam
 
     if (++plocal == ppages) {
       // Sequence pb ends inside this range.
-      finalize(seg0 == 0);
+      if (!sliced) finalize(seg0 == 0);
       if (idx + 1 < count) {
         do {
           ++pb;
@@ -402,7 +405,59 @@ __global__ __launch_bounds__(64 * kMaxWaves, 3) void paged_attn_kernel(AttnParam
     process(idx + 1, kb2, vb2, okb);
   }
   // The range ended inside sequence pb: leave a partial.
-  if (plocal != ppages) finalize(false);
+  if (!sliced) {
+    if (plocal != ppages) finalize(false);
+    return;
+  }
+
+  // Sliced mode: combine the waves' states.  Each wave stores (m, l, acc) of
+  // its 16 head columns; wave w then merges head columns 4w .. 4w+3 with lane
+  // = (column 4w + lane/16, dims (lane%16)*D/16 ..).  Empty sequences and
+  // empty slices carry m = -inf, l = 0 and give weight 0 (all-empty: zeros,
+  // src/paged_gqa.cu:63).
+  float lt = l + shfl_xor_f(l, 16);
+  lt += shfl_xor_f(lt, 32);
+  __syncthreads();  // K/V staging is reused below
+  float* xs = reinterpret_cast<float*>(s_mem);           // [wave][16][XP]
+  float* xml = xs + (size_t)kMaxWaves * 16 * XP;          // [wave][16][2]
+#pragma unroll
+  for (int t = 0; t < DT; ++t)
+    *reinterpret_cast<float4*>(xs + ((size_t)wave * 16 + c16) * XP + 16 * t + 4 * g4) =
+        make_float4(acc[t][0], acc[t][1], acc[t][2], acc[t][3]);
+  if (g4 == 0) {
+    xml[(wave * 16 + c16) * 2] = m == kNegInf ? kNegInf : m * c;
+    xml[(wave * 16 + c16) * 2 + 1] = lt;
+  }
+  __syncthreads();
+  constexpr int DL = D / 16;  // dims per lane
+  const int col = 4 * wave + (lane >> 4), d0 = (lane & 15) * DL;
+  float mx = kNegInf;
+  for (int w = 0; w < P.waves; ++w) mx = __builtin_fmaxf(mx, xml[(w * 16 + col) * 2]);
+  float o[DL], lsum = 0.f;
+#pragma unroll
+  for (int j = 0; j < DL; ++j) o[j] = 0.f;
+  for (int w = 0; w < P.waves; ++w) {
+    const float mw = xml[(w * 16 + col) * 2];
+    const float wt = mw == kNegInf ? 0.f : fast_exp2(mw - mx);
+    lsum += wt * xml[(w * 16 + col) * 2 + 1];
+    const float* src = xs + ((size_t)w * 16 + col) * XP + d0;
+#pragma unroll
+    for (int j = 0; j < DL; j += 4) {
+      const float4 v4 = *reinterpret_cast<const float4*>(src + j);
+      o[j] += wt * v4.x;
+      o[j + 1] += wt * v4.y;
+      o[j + 2] += wt * v4.z;
+      o[j + 3] += wt * v4.w;
+    }
+  }
+  if (col < nh) {
+    const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+    const size_t off = ((size_t)pb * P.hq + h0 + col) * D + d0;
+#pragma unroll
+    for (int j = 0; j < DL; j += 4)
+      store4<OutT>(P.out, off + j, o[j] * inv, o[j + 1] * inv, o[j + 2] * inv,
+                   o[j + 3] * inv);
+  }
 }
 
 // Flat mode: out = sum_w 2^(m_w - M) a_w / sum_w 2^(m_w - M) l_w over the
@@ -492,8 +547,7 @@ void launch_attn(const AttnParams& P, dim3 grid, hipStream_t st) {
 template <int D, typename OutT>
 hipError_t launch_dim(const AttnParams& P, bool vec, hipStream_t st) {
   const int zgroups = (P.zdim + P.waves - 1) / P.waves;
-  const int ranges = P.nwg > 0 ? P.nwg : P.batch;
-  const dim3 grid((unsigned)((size_t)ranges * zgroups));
+  const dim3 grid((unsigned)(P.nwg > 0 ? (size_t)P.nwg * zgroups : (size_t)P.batch * P.zdim));
   if (vec) launch_attn<D, OutT, true>(P, grid, st);
   else launch_attn<D, OutT, false>(P, grid, st);
   hipError_t err = hipGetLastError();
@@ -512,7 +566,9 @@ hipError_t launch(AttnParams& P, int dim, hipStream_t st) {
   P.group = P.hq / P.hkv;
   P.nblk = (P.group + kHeadCols - 1) / kHeadCols;
   P.zdim = P.hkv * P.nblk;
-  P.waves = P.zdim < kMaxWaves ? P.zdim : kMaxWaves;
+  // Flat mode: one wave per head block, up to four per workgroup.  Sliced
+  // mode: four waves on one head block, each on a quarter of the pages.
+  P.waves = P.nwg == 0 || P.zdim >= kMaxWaves ? kMaxWaves : P.zdim;
   const bool vec = aligned16(P.q) && aligned16(P.kbase) &&
                    aligned16(P.vbase) &&
                    (P.page_stride | P.head_stride | P.slot_stride) % 8 == 0;
