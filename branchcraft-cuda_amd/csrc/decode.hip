@@ -53,6 +53,9 @@ typedef short i16x4 __attribute__((ext_vector_type(4)));
 // Four waves per workgroup at <= 168 VGPRs: up to three workgroups share a
 // CU, so a CU keeps 8-12 waves of page loads in flight.
 constexpr int kMaxWaves = 4;
+// Waves per workgroup without a workspace: one (sequence, head block) per
+// workgroup, the pages split kSlices ways and merged through LDS.
+constexpr int kSlices = 8;
 constexpr int kHeadCols = 16;  // MFMA N: query heads of one KV head per wave
 
 struct AttnParams {
@@ -170,8 +173,10 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-template <int D, typename OutT, bool VEC>
-__global__ __launch_bounds__(64 * kMaxWaves, 3) void paged_attn_kernel(AttnParams P) {
+// WAVES: waves per workgroup (4 in flat mode, kSlices in sliced mode).
+template <int D, typename OutT, bool VEC, int WAVES>
+__global__ __launch_bounds__(64 * WAVES, WAVES == kMaxWaves ? 3 : 2) void paged_attn_kernel(
+    AttnParams P) {
   constexpr int KS = D / 32;   // QK k-steps (and 16-byte loads per page row set)
   constexpr int DT = D / 16;   // 16-dim output tiles
   constexpr int VP = D + 16;   // halves per staged V row
@@ -182,11 +187,11 @@ __global__ __launch_bounds__(64 * kMaxWaves, 3) void paged_attn_kernel(AttnParam
   // Per-wave K/V staging; reused after the page loop by the sliced mode's
   // merge of [wave][head][D + 4] FP32 states.
   constexpr int XP = D + 4;
-  constexpr size_t kStage = (size_t)kMaxWaves * 16 * (VP + KP) * 2;
-  constexpr size_t kMerge = (size_t)kMaxWaves * 16 * (XP + 2) * 4;
+  constexpr size_t kStage = (size_t)WAVES * 16 * (VP + KP) * 2;
+  constexpr size_t kMerge = (size_t)WAVES * 16 * (XP + 2) * 4;
   __shared__ __attribute__((aligned(16))) char s_mem[kStage > kMerge ? kStage : kMerge];
   _Float16* const s_v = reinterpret_cast<_Float16*>(s_mem);
-  _Float16* const s_k = s_v + kMaxWaves * 16 * VP;
+  _Float16* const s_k = s_v + WAVES * 16 * VP;
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -196,7 +201,7 @@ __global__ __launch_bounds__(64 * kMaxWaves, 3) void paged_attn_kernel(AttnParam
   // blockIdx.x = range * zgroups + zg; wave -> head block z.
   // Flat mode: blockIdx.x = range * zgroups + zg, wave -> head block z.
   // Sliced mode (nwg == 0): blockIdx.x = sequence * zdim + z, every wave on
-  // head block z, wave w on the w-th quarter of the sequence's pages.
+  // head block z, wave w on the w-th of WAVES shares of the sequence's pages.
   const bool sliced = P.nwg == 0;
   const int zgroups = (P.zdim + P.waves - 1) / P.waves;
   const int rid = sliced ? blockIdx.x / P.zdim : blockIdx.x / zgroups;
@@ -213,8 +218,8 @@ __global__ __launch_bounds__(64 * kMaxWaves, 3) void paged_attn_kernel(AttnParam
   if (sliced) {
     pb = rid;
     const int np = seq_pages(P, pb);
-    plocal = wave * np / P.waves;
-    count = (wave + 1) * np / P.waves - plocal;  // may be 0 (an empty slice)
+    plocal = wave * np / WAVES;
+    count = (wave + 1) * np / WAVES - plocal;  // may be 0 (an empty slice)
   } else {
     int total, per;
     flat_geometry(P, lane, total, per);
@@ -411,15 +416,15 @@ __global__ __launch_bounds__(64 * kMaxWaves, 3) void paged_attn_kernel(AttnParam
   }
 
   // Sliced mode: combine the waves' states.  Each wave stores (m, l, acc) of
-  // its 16 head columns; wave w then merges head columns 4w .. 4w+3 with lane
-  // = (column 4w + lane/16, dims (lane%16)*D/16 ..).  Empty sequences and
-  // empty slices carry m = -inf, l = 0 and give weight 0 (all-empty: zeros,
-  // src/paged_gqa.cu:63).
+  // its 16 head columns; wave w then merges CPW = 16/WAVES of the columns,
+  // lane = (column CPW*w + lane/LPC, dims (lane%LPC)*DL ..).  Empty sequences
+  // and empty slices carry m = -inf, l = 0 and give weight 0 (all-empty:
+  // zeros, src/paged_gqa.cu:63).
   float lt = l + shfl_xor_f(l, 16);
   lt += shfl_xor_f(lt, 32);
   __syncthreads();  // K/V staging is reused below
   float* xs = reinterpret_cast<float*>(s_mem);           // [wave][16][XP]
-  float* xml = xs + (size_t)kMaxWaves * 16 * XP;          // [wave][16][2]
+  float* xml = xs + (size_t)WAVES * 16 * XP;              // [wave][16][2]
 #pragma unroll
   for (int t = 0; t < DT; ++t)
     *reinterpret_cast<float4*>(xs + ((size_t)wave * 16 + c16) * XP + 16 * t + 4 * g4) =
@@ -429,34 +434,33 @@ __global__ __launch_bounds__(64 * kMaxWaves, 3) void paged_attn_kernel(AttnParam
     xml[(wave * 16 + c16) * 2 + 1] = lt;
   }
   __syncthreads();
-  constexpr int DL = D / 16;  // dims per lane
-  const int col = 4 * wave + (lane >> 4), d0 = (lane & 15) * DL;
+  constexpr int CPW = 16 / WAVES;  // head columns merged per wave
+  constexpr int LPC = 64 / CPW;    // lanes per column
+  constexpr int DL = D / LPC;      // dims per lane
+  static_assert(DL % 2 == 0, "at least float2 merge steps");
+  const int col = CPW * wave + lane / LPC, d0 = (lane % LPC) * DL;
   float mx = kNegInf;
-  for (int w = 0; w < P.waves; ++w) mx = __builtin_fmaxf(mx, xml[(w * 16 + col) * 2]);
+  for (int w = 0; w < WAVES; ++w) mx = __builtin_fmaxf(mx, xml[(w * 16 + col) * 2]);
   float o[DL], lsum = 0.f;
 #pragma unroll
   for (int j = 0; j < DL; ++j) o[j] = 0.f;
-  for (int w = 0; w < P.waves; ++w) {
+  for (int w = 0; w < WAVES; ++w) {
     const float mw = xml[(w * 16 + col) * 2];
     const float wt = mw == kNegInf ? 0.f : fast_exp2(mw - mx);
     lsum += wt * xml[(w * 16 + col) * 2 + 1];
     const float* src = xs + ((size_t)w * 16 + col) * XP + d0;
 #pragma unroll
-    for (int j = 0; j < DL; j += 4) {
-      const float4 v4 = *reinterpret_cast<const float4*>(src + j);
-      o[j] += wt * v4.x;
-      o[j + 1] += wt * v4.y;
-      o[j + 2] += wt * v4.z;
-      o[j + 3] += wt * v4.w;
+    for (int j = 0; j < DL; j += 2) {
+      const float2 v2 = *reinterpret_cast<const float2*>(src + j);
+      o[j] += wt * v2.x;
+      o[j + 1] += wt * v2.y;
     }
   }
   if (col < nh) {
     const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
     const size_t off = ((size_t)pb * P.hq + h0 + col) * D + d0;
 #pragma unroll
-    for (int j = 0; j < DL; j += 4)
-      store4<OutT>(P.out, off + j, o[j] * inv, o[j + 1] * inv, o[j + 2] * inv,
-                   o[j + 3] * inv);
+    for (int j = 0; j < DL; ++j) store_out<OutT>(P.out, off + j, o[j] * inv);
   }
 }
 
@@ -541,7 +545,10 @@ bool shape_ok(const bc_shape& s) {
 
 template <int D, typename OutT, bool VEC>
 void launch_attn(const AttnParams& P, dim3 grid, hipStream_t st) {
-  paged_attn_kernel<D, OutT, VEC><<<grid, dim3(64 * P.waves), 0, st>>>(P);
+  if (P.nwg == 0)
+    paged_attn_kernel<D, OutT, VEC, kSlices><<<grid, dim3(64 * kSlices), 0, st>>>(P);
+  else
+    paged_attn_kernel<D, OutT, VEC, kMaxWaves><<<grid, dim3(64 * P.waves), 0, st>>>(P);
 }
 
 template <int D, typename OutT>
@@ -567,8 +574,8 @@ hipError_t launch(AttnParams& P, int dim, hipStream_t st) {
   P.nblk = (P.group + kHeadCols - 1) / kHeadCols;
   P.zdim = P.hkv * P.nblk;
   // Flat mode: one wave per head block, up to four per workgroup.  Sliced
-  // mode: four waves on one head block, each on a quarter of the pages.
-  P.waves = P.nwg == 0 || P.zdim >= kMaxWaves ? kMaxWaves : P.zdim;
+  // mode: kSlices waves on one head block, each on a share of the pages.
+  P.waves = P.nwg == 0 ? kSlices : P.zdim >= kMaxWaves ? kMaxWaves : P.zdim;
   const bool vec = aligned16(P.q) && aligned16(P.kbase) &&
                    aligned16(P.vbase) &&
                    (P.page_stride | P.head_stride | P.slot_stride) % 8 == 0;
@@ -644,13 +651,18 @@ extern "C" int bc_decode(bc_shape s, bc_inputs in, bc_scratch scratch,
 }
 
 extern "C" int bc_auto_splits(bc_shape s, int max_length, int cu_count) {
-  // Split decode runs flat page ranges: (splits - 1) * batch + 1 workgroups
-  // share all pages equally.  Pick the largest split count whose workgroups
-  // fit one workgroup per CU; contexts under 64 tokens stay in one workgroup.
-  if (max_length < 64 || s.batch < 1 || s.kv_heads < 1 || s.query_heads < 1 ||
-      s.query_heads % s.kv_heads)
+  // splits == 1 runs one workgroup per (sequence, head block) with the pages
+  // split kSlices ways inside it and no merge kernel: the faster choice while
+  // every slice is short (contexts up to 1024 tokens) and those workgroups fit
+  // the CUs at once.  Otherwise split decode runs flat page ranges: (splits -
+  // 1) * batch + 1 workgroups share all pages equally; pick the largest split
+  // count whose workgroups fit one per CU.
+  if (s.batch < 1 || s.kv_heads < 1 || s.query_heads < 1 || s.query_heads % s.kv_heads)
     return 1;
   const int cus = cu_count > 0 ? cu_count : 256;
+  const int group = s.query_heads / s.kv_heads;
+  const long long zdim = (long long)s.kv_heads * ((group + kHeadCols - 1) / kHeadCols);
+  if (max_length <= 1024 && (long long)s.batch * zdim <= cus) return 1;
   const int per_wave = cus / zgroups_of(s);
   long long splits = per_wave > 1 ? (per_wave - 1) / s.batch + 1 : 1;
   if (splits > BC_MAX_SPLITS) splits = BC_MAX_SPLITS;

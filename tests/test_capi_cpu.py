@@ -136,9 +136,16 @@ def test_packed_rejects(strides, scale):
 def test_auto_splits_policy():
     """Split decode runs (splits - 1) * batch + 1 flat page ranges, each
     served by ceil(kv head blocks / 4) four-wave workgroups; the heuristic
-    picks the most ranges whose workgroups fit one per CU."""
+    picks the most ranges whose workgroups fit one per CU, and keeps short
+    contexts unsplit."""
     lib = capi.load()
     assert lib.bc_auto_splits(_shape(batch=1), 63, 256) == 1  # tiny contexts stay whole
+    # short contexts whose (sequence, head block) workgroups fit the CUs run
+    # unsplit: eight waves share each sequence's pages, no merge kernel
+    assert lib.bc_auto_splits(_shape(batch=1), 512, 256) == 1
+    assert lib.bc_auto_splits(_shape(batch=32), 1024, 256) == 1
+    assert lib.bc_auto_splits(_shape(batch=33), 1024, 256) > 1
+    assert lib.bc_auto_splits(_shape(batch=1), 1025, 256) > 1
     ranges = 256 // 2  # 8 KV heads: two four-wave workgroups per range
     for batch in (1, 4, 16, 64, 200):
         s = lib.bc_auto_splits(_shape(batch=batch), 32768, 256)
