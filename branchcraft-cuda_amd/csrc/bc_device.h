@@ -11,6 +11,9 @@ namespace bcd {
 
 constexpr float kNegInf = -__builtin_huge_valf();
 constexpr float kLog2e = 1.4426950408889634f;
+// Online softmax: the running max is moved (and the accumulators rescaled)
+// only when it would grow by more than this many log2 units.
+constexpr float kRescaleSlack = 8.f;
 
 __device__ __forceinline__ float fast_exp2(float x) {
   return __builtin_amdgcn_exp2f(x);  // v_exp_f32; exp2(-inf) == 0

@@ -211,6 +211,7 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == kMaxWaves ? 3 : 2) void paged_
   const int h0 = kvh * P.group + (z % P.nblk) * kHeadCols;
   const int nh = min(kHeadCols, P.group - (z % P.nblk) * kHeadCols);
   const float c = P.scale_log2;
+  const float slack_raw = kRescaleSlack / c;  // the slack in raw score units
 
   // This workgroup's pages: sequence pb from local page `plocal`, `count`
   // pages in all (crossing into later sequences in flat mode).
@@ -352,8 +353,11 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == kMaxWaves ? 3 : 2) void paged_
     float tmax = __builtin_fmaxf(__builtin_fmaxf(sv[0], sv[1]), __builtin_fmaxf(sv[2], sv[3]));
     tmax = __builtin_fmaxf(tmax, shfl_xor_f(tmax, 16));
     tmax = __builtin_fmaxf(tmax, shfl_xor_f(tmax, 32));
+    // The running max moves only when it would grow by more than
+    // kRescaleSlack in log2 units (weights stay below 2^kRescaleSlack), so
+    // most pages skip rescaling the accumulators.
     const float mnew = __builtin_fmaxf(m, tmax);
-    if (__builtin_amdgcn_ballot_w64(mnew > m)) {
+    if (__builtin_amdgcn_ballot_w64(mnew > m + slack_raw)) {
       const float alpha = fast_exp2((m - safe_max(mnew)) * c);
       l *= alpha;
 #pragma unroll

@@ -279,8 +279,11 @@ __global__ __launch_bounds__(kThreads) void tree_kernel(TreeParams P) {
       tmax = __builtin_fmaxf(tmax, sv[j]);
     }
     tmax = __builtin_fmaxf(tmax, shfl_xor_f(tmax, 32));
+    // The running max moves only when it would grow by more than
+    // kRescaleSlack (log2 units): weights then stay below 2^kRescaleSlack and
+    // most tiles skip rescaling the accumulators.
     const float mnew = __builtin_fmaxf(m, tmax);
-    if (__builtin_amdgcn_ballot_w64(mnew > m)) {
+    if (__builtin_amdgcn_ballot_w64(mnew > m + kRescaleSlack)) {
       const float alpha = fast_exp2(m - safe_max(mnew));
       l *= alpha;
 #pragma unroll
