@@ -87,7 +87,7 @@ __device__ __forceinline__ size_t slot_index(const TreeParams& P, int b,
 }
 
 template <int D>
-__global__ __launch_bounds__(kThreads) void tree_kernel(TreeParams P) {
+__global__ __launch_bounds__(kThreads, 2) void tree_kernel(TreeParams P) {
   constexpr int KS = D / 16;  // MFMA k-steps over the head dimension
   constexpr int DT = D / 32;  // 32-row output tiles over the head dimension
   constexpr int VP = v_pitch<D>();
@@ -140,17 +140,17 @@ __global__ __launch_bounds__(kThreads) void tree_kernel(TreeParams P) {
   const bool rvalid = r < P.rows;
   const int node = rvalid ? r / P.group : 0;
   const int h = kvh * P.group + (rvalid ? r % P.group : 0);
-  uint4 qreg[KS];
-  {
-    const uint16_t* qp = P.dq + (((size_t)b * P.nodes + node) * P.hq + h) * D + 8 * g;
-#pragma unroll
-    for (int s = 0; s < KS; ++s)
-      qreg[s] = rvalid ? ldg16(qp + 16 * s) : make_uint4(0, 0, 0, 0);
-  }
-
+  // Q^T B operand fragments, the same for every wave of the workgroup: wave
+  // 0 stages them in LDS (lane-major per k-step), all waves read them back.
+  __shared__ uint4 s_q[KS][64];
   __shared__ int s_parent[BC_MAX_TREE_NODES];
   __shared__ __attribute__((aligned(16))) char s_mem[kWaves * kTile * VP * 2];
   __shared__ float s_m[2][32], s_l[2][32];
+  if (wave == 0) {
+    const uint16_t* qp = P.dq + (((size_t)b * P.nodes + node) * P.hq + h) * D + 8 * g;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) s_q[s][lane] = rvalid ? ldg16(qp + 16 * s) : make_uint4(0, 0, 0, 0);
+  }
   if (drafts)
     for (int i = threadIdx.x; i < P.nodes; i += kThreads)
       s_parent[i] = P.parent[(size_t)b * P.nodes + i];
@@ -186,11 +186,12 @@ __global__ __launch_bounds__(kThreads) void tree_kernel(TreeParams P) {
       ph[q] = it < ntile_p && pg < P.max_pages ? P.pages[(size_t)b * P.max_pages + pg] : -1;
     }
   };
-  auto issue = [&](int idx, const int (&ph)[2], uint4 (&kr)[KS], uint4 (&vr)[KS], bool& tv,
+  // K is loaded one tile ahead; V is requested when its tile starts and is
+  // consumed after the scores and softmax.
+  auto issue = [&](int idx, const int (&ph)[2], uint4 (&kr)[KS], const uint16_t*& vp, bool& tv,
                    bool (&pok)[2]) {
     const int it = tile_of(idx);
     const uint16_t* kp;
-    const uint16_t* vp;
     if (it < ntile_p) {
       const int tbase = (tp0 + it) * kTile;
 #pragma unroll
@@ -211,15 +212,15 @@ __global__ __launch_bounds__(kThreads) void tree_kernel(TreeParams P) {
       vp = P.dv + off;
     }
 #pragma unroll
-    for (int s = 0; s < KS; ++s) {
-      kr[s] = ldg16(kp + 16 * s + 8 * g);
-      vr[s] = ldg16(vp + 16 * s + 8 * g);
-    }
+    for (int s = 0; s < KS; ++s) kr[s] = ldg16(kp + 16 * s + 8 * g);
   };
 
-  auto process = [&](int idx, const uint4 (&kr)[KS], uint4 (&vr)[KS], bool tv,
+  auto process = [&](int idx, const uint4 (&kr)[KS], const uint16_t* vp, bool tv,
                      const bool (&pok)[2]) {
     if (idx >= nmine) return;  // padding step
+    uint4 vr[KS];
+#pragma unroll
+    for (int s = 0; s < KS; ++s) vr[s] = ldg16(vp + 16 * s + 8 * g);
     const int it = wave + kWaves * idx;
     const bool is_draft = it >= ntile_p;
     const int tbase = is_draft ? (it - ntile_p) * kTile : (tp0 + it) * kTile;
@@ -260,7 +261,7 @@ __global__ __launch_bounds__(kThreads) void tree_kernel(TreeParams P) {
 #pragma unroll
     for (int s = 0; s < KS; ++s)
       sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_f16x8(kr[s]),
-                                                  as_f16x8(qreg[s]), sc, 0, 0, 0);
+                                                  as_f16x8(s_q[s][lane]), sc, 0, 0, 0);
 
     // ---- stage V row-major while the MFMAs drain ----
 #pragma unroll
@@ -325,7 +326,9 @@ __global__ __launch_bounds__(kThreads) void tree_kernel(TreeParams P) {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   };
 
-  uint4 ka[KS], va[KS], kb[KS], vb[KS];
+  uint4 ka[KS], kb[KS];
+  const uint16_t* va = P.v;
+  const uint16_t* vb = P.v;
   bool ta = false, tb = false;
   bool pa[2] = {true, true}, pbk[2] = {true, true};
   int idb[2];
