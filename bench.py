@@ -391,7 +391,9 @@ def bench_tree(cx, batch, prefix, seed, with_expanded):
 
 def bench_commit(cx, f):
     """Config 3 commit: each request clones the shared partial page, then
-    writes a random root-to-leaf path (device work of PagedTreeCache.commit)."""
+    writes a random root-to-leaf path.  Two launches, as
+    PagedTreeCache.commit_many issues them: every clone (bc_copy_pages), then
+    every accepted node of every request (bc_commit_paths)."""
     t = cx.torch
     capi = cx.capi
     rng = np.random.default_rng(303)
@@ -402,30 +404,33 @@ def bench_commit(cx, f):
     dst = t.tensor(fresh, device="cuda", dtype=t.int32)
     shape = capi.Shape(b, hkv, hkv, d, 1, f["pool"])
     k, v = f["k"].clone(), f["v"].clone()
-    plans = []
+    rows = []
     for bi in range(b):
         par = f["parent_np"][bi]
         leaves = [x for x in range(n) if x not in set(par.tolist())]
         path = ancestors(par, int(rng.choice(leaves)))[::-1]
-        pos = range(L, L + len(path))
-        dp = [fresh[bi] if p // PAGE == (L - 1) // PAGE else fresh[bi] for p in pos]
-        ds = [p % PAGE for p in pos]
-        plans.append(tuple(t.tensor(x, device="cuda", dtype=t.int32) for x in (path, dp, ds))
-                     + (len(path),))
+        for j, node in enumerate(path):
+            pos = L + j
+            page = fresh[bi] if pos // PAGE == (L - 1) // PAGE else -1
+            rows.append((bi, node, page, pos % PAGE))
+    if any(r[2] < 0 for r in rows):
+        raise RuntimeError("config 3 paths must fit the cloned partial page")
+    reqs, nodes, pages, slots = (t.tensor([r[j] for r in rows], device="cuda", dtype=t.int32)
+                                 for j in range(4))
     lib, st = cx.lib, cx.stream()
 
     def call():
         err = lib.bc_copy_pages(shape, k.data_ptr(), v.data_ptr(), src.data_ptr(),
                                 dst.data_ptr(), b, st)
-        for bi, (tp, tdp, tds, m) in enumerate(plans):
-            err |= lib.bc_commit_path(shape, f["dk"].data_ptr(), f["dv"].data_ptr(),
-                                      k.data_ptr(), v.data_ptr(), tp.data_ptr(),
-                                      tdp.data_ptr(), tds.data_ptr(), bi, n, m, st)
+        err |= lib.bc_commit_paths(shape, f["dk"].data_ptr(), f["dv"].data_ptr(),
+                                   k.data_ptr(), v.data_ptr(), reqs.data_ptr(),
+                                   nodes.data_ptr(), pages.data_ptr(), slots.data_ptr(),
+                                   n, len(rows), st)
         if err:
             raise RuntimeError("commit failed")
     us = median_us(t, call)
-    moved = 2 * b * PAGE * hkv * d * 2 * 2 + 2 * sum(p[3] for p in plans) * hkv * d * 2 * 2
-    return {"us": round(us, 3), "bytes": moved, "launches": 1 + b}
+    moved = 2 * b * PAGE * hkv * d * 2 * 2 + 2 * len(rows) * hkv * d * 2 * 2
+    return {"us": round(us, 3), "bytes": moved, "launches": 2, "accepted_nodes": len(rows)}
 
 
 # ---------------------------------------------------------------------------

@@ -3,6 +3,8 @@
 // Reference: commit_kernel / commit_path (src/tree_attention.cu:73-89,
 // 107-122) and the page clone done with cudaMemcpy D2D (src/main.cu:276-281)
 // or torch copy_ (python/branchcraft_torch/transaction.py:133-134).
+// bc_commit_paths commits the accepted paths of several requests in one
+// launch; bc_copy_pages clones any number of pages in one launch.
 // Both are bit copies of FP16 rows moved as 16-byte vectors; every index is
 // range-checked on the device and an out-of-range entry is skipped rather
 // than written out of bounds.
@@ -12,20 +14,22 @@ namespace {
 
 constexpr int kThreads = 256;
 
-// One workgroup per accepted node; K and V rows of Hkv*D halves each.
+// One workgroup per accepted node; K and V rows of Hkv*D halves each.  The
+// node's request is `requests[i]` when a list is given, else `request`.
 __global__ __launch_bounds__(kThreads) void commit_kernel(
     const uint4* __restrict__ draft_k, const uint4* __restrict__ draft_v,
     uint4* __restrict__ cache_k, uint4* __restrict__ cache_v,
-    const int32_t* __restrict__ path_nodes,
+    const int32_t* __restrict__ requests, const int32_t* __restrict__ path_nodes,
     const int32_t* __restrict__ dest_pages,
-    const int32_t* __restrict__ dest_slots, int request, int nodes,
+    const int32_t* __restrict__ dest_slots, int request, int batch, int nodes,
     int phys_pages, int row_vec) {
   const int i = blockIdx.x;
+  if (requests) request = requests[i];
   const int node = path_nodes[i];
   const int page = dest_pages[i];
   const int slot = dest_slots[i];
-  if (node < 0 || node >= nodes || page < 0 || page >= phys_pages || slot < 0 ||
-      slot >= BC_PAGE_SIZE)
+  if (request < 0 || request >= batch || node < 0 || node >= nodes || page < 0 ||
+      page >= phys_pages || slot < 0 || slot >= BC_PAGE_SIZE)
     return;
   const size_t src = ((size_t)request * nodes + node) * row_vec;
   const size_t dst = ((size_t)page * BC_PAGE_SIZE + slot) * row_vec;
@@ -80,8 +84,31 @@ extern "C" int bc_commit_path(bc_shape s, const bc_half* draft_k,
                   reinterpret_cast<hipStream_t>(stream)>>>(
       reinterpret_cast<const uint4*>(draft_k),
       reinterpret_cast<const uint4*>(draft_v), reinterpret_cast<uint4*>(cache_k),
-      reinterpret_cast<uint4*>(cache_v), path_nodes, dest_pages, dest_slots,
-      request, nodes, s.physical_pages, row_vec);
+      reinterpret_cast<uint4*>(cache_v), nullptr, path_nodes, dest_pages, dest_slots,
+      request, s.batch, nodes, s.physical_pages, row_vec);
+  return hipGetLastError();
+}
+
+extern "C" int bc_commit_paths(bc_shape s, const bc_half* draft_k,
+                               const bc_half* draft_v, bc_half* cache_k,
+                               bc_half* cache_v, const int32_t* requests,
+                               const int32_t* path_nodes,
+                               const int32_t* dest_pages,
+                               const int32_t* dest_slots, int nodes, int count,
+                               bc_stream_t stream) {
+  if (!draft_k || !draft_v || !cache_k || !cache_v || !requests || !path_nodes ||
+      !dest_pages || !dest_slots || s.batch < 1 || nodes < 1 || count < 0 ||
+      s.kv_heads < 1 || s.physical_pages < 1 || (s.dim != 64 && s.dim != 128))
+    return BC_ERROR_INVALID_VALUE;
+  if (!aligned16(draft_k) || !aligned16(draft_v) || !aligned16(cache_k) ||
+      !aligned16(cache_v))
+    return BC_ERROR_INVALID_VALUE;
+  if (count == 0) return BC_SUCCESS;
+  const int row_vec = s.kv_heads * s.dim / 8;
+  commit_kernel<<<dim3(count), kThreads, 0, reinterpret_cast<hipStream_t>(stream)>>>(
+      reinterpret_cast<const uint4*>(draft_k), reinterpret_cast<const uint4*>(draft_v),
+      reinterpret_cast<uint4*>(cache_k), reinterpret_cast<uint4*>(cache_v), requests,
+      path_nodes, dest_pages, dest_slots, 0, s.batch, nodes, s.physical_pages, row_vec);
   return hipGetLastError();
 }
 

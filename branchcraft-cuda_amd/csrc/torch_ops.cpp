@@ -192,6 +192,48 @@ void commit_path_hip(at::Tensor& cache_k, at::Tensor& cache_v,
                "commit_path_");
 }
 
+// Accepted paths of several requests in one launch (no reference op: it
+// batches the per-request commit_path_ calls of a transaction,
+// python/branchcraft_torch/transaction.py:144-148).
+void commit_paths_hip(at::Tensor& cache_k, at::Tensor& cache_v,
+                      const at::Tensor& draft_k, const at::Tensor& draft_v,
+                      const at::Tensor& requests, const at::Tensor& path_nodes,
+                      const at::Tensor& dest_pages, const at::Tensor& dest_slots) {
+  check_dev_contig(cache_k, "cache_k", at::kHalf);
+  check_dev_contig(cache_v, "cache_v", at::kHalf);
+  check_dev_contig(draft_k, "draft_k", at::kHalf);
+  check_dev_contig(draft_v, "draft_v", at::kHalf);
+  check_dev_contig(requests, "requests", at::kInt);
+  check_dev_contig(path_nodes, "path_nodes", at::kInt);
+  check_dev_contig(dest_pages, "dest_pages", at::kInt);
+  check_dev_contig(dest_slots, "dest_slots", at::kInt);
+  TORCH_CHECK(cache_k.dim() == 4 && cache_v.sizes() == cache_k.sizes() &&
+                  draft_k.dim() == 4 && draft_v.sizes() == draft_k.sizes() &&
+                  requests.dim() == 1 && path_nodes.sizes() == requests.sizes() &&
+                  dest_pages.sizes() == requests.sizes() &&
+                  dest_slots.sizes() == requests.sizes(),
+              "commit tensor shape mismatch");
+  const int64_t b = draft_k.size(0), nodes = draft_k.size(1), hkv = draft_k.size(2);
+  const int64_t d = draft_k.size(3);
+  TORCH_CHECK(b > 0 && nodes > 0 && cache_k.size(1) == BC_PAGE_SIZE &&
+                  cache_k.size(2) == hkv && cache_k.size(3) == d,
+              "invalid commit destination");
+  TORCH_CHECK(cache_k.device() == draft_k.device() && cache_k.device() == cache_v.device() &&
+                  cache_k.device() == draft_v.device() &&
+                  cache_k.device() == requests.device() &&
+                  cache_k.device() == path_nodes.device() &&
+                  cache_k.device() == dest_pages.device() &&
+                  cache_k.device() == dest_slots.device(),
+              "all tensors must share a device");
+  bc_shape shape{int(b), int(hkv), int(hkv), int(d), 1, int(cache_k.size(0))};
+  check_launch(bc_commit_paths(shape, hptr(draft_k), hptr(draft_v), hptr_mut(cache_k),
+                               hptr_mut(cache_v), requests.data_ptr<int>(),
+                               path_nodes.data_ptr<int>(), dest_pages.data_ptr<int>(),
+                               dest_slots.data_ptr<int>(), int(nodes),
+                               int(requests.numel()), current_stream()),
+               "commit_paths_");
+}
+
 // Copy-on-write page clone (no reference op: the reference transaction uses
 // torch copy_, python/branchcraft_torch/transaction.py:133-134).
 void copy_pages_hip(at::Tensor& cache_k, at::Tensor& cache_v,
@@ -223,6 +265,7 @@ TORCH_LIBRARY(branchcraft, m) {
   m.def("packed_decode_out(Tensor q, Tensor packed_kv, Tensor pages, Tensor lengths, Tensor(a!) output, float scale) -> Tensor(a!)");
   m.def("commit_path_(Tensor(a!) cache_k, Tensor(b!) cache_v, Tensor draft_k, Tensor draft_v, Tensor path_nodes, Tensor dest_pages, Tensor dest_slots, int request) -> ()");
   m.def("copy_pages_(Tensor(a!) cache_k, Tensor(b!) cache_v, Tensor src_pages, Tensor dst_pages) -> ()");
+  m.def("commit_paths_(Tensor(a!) cache_k, Tensor(b!) cache_v, Tensor draft_k, Tensor draft_v, Tensor requests, Tensor path_nodes, Tensor dest_pages, Tensor dest_slots) -> ()");
 }
 
 TORCH_LIBRARY_IMPL(branchcraft, CUDA, m) {
@@ -230,4 +273,5 @@ TORCH_LIBRARY_IMPL(branchcraft, CUDA, m) {
   m.impl("packed_decode_out", packed_decode_out_hip);
   m.impl("commit_path_", commit_path_hip);
   m.impl("copy_pages_", copy_pages_hip);
+  m.impl("commit_paths_", commit_paths_hip);
 }

@@ -26,7 +26,7 @@ BC_MAX_TREE_NODES = 256
 EXPORTED = (
     "bc_decode", "bc_auto_splits", "bc_tree_verify",
     "bc_tree_verify_workspace_size", "bc_tree_verify_ws", "bc_commit_path",
-    "bc_copy_pages", "bc_packed_decode", "bc_packed_decode_workspace_size",
+    "bc_commit_paths", "bc_copy_pages", "bc_packed_decode", "bc_packed_decode_workspace_size",
     "bc_packed_decode_ws", "bc_version",
 )
 
@@ -76,6 +76,10 @@ def load(path: str | Path | None = None) -> ctypes.CDLL:
                                    c_void_p, c_void_p, c_void_p, c_int, c_int, c_int,
                                    c_void_p]
     lib.bc_commit_path.restype = c_int
+    lib.bc_commit_paths.argtypes = [Shape, c_void_p, c_void_p, c_void_p, c_void_p,
+                                    c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int,
+                                    c_void_p]
+    lib.bc_commit_paths.restype = c_int
     lib.bc_copy_pages.argtypes = [Shape, c_void_p, c_void_p, c_void_p, c_void_p,
                                   c_int, c_void_p]
     lib.bc_copy_pages.restype = c_int

@@ -44,6 +44,12 @@ def _fake_copy_pages(cache_k, cache_v, src_pages, dst_pages):
     return None
 
 
+@torch.library.register_fake("branchcraft::commit_paths_")
+def _fake_commit_paths(cache_k, cache_v, draft_k, draft_v, requests, path_nodes,
+                       dest_pages, dest_slots):
+    return None
+
+
 def tree_verify(q, prefix_k, prefix_v, pages, lengths, draft_k, draft_v, parent):
     """FP32 [batch, node, query head, dim] outputs; every node attends to its
     request's paged prefix and its own ancestor chain (itself included)."""
@@ -72,5 +78,13 @@ def copy_pages_(cache_k, cache_v, src_pages, dst_pages):
     return torch.ops.branchcraft.copy_pages_(cache_k, cache_v, src_pages, dst_pages)
 
 
-__all__ = ["tree_verify", "packed_decode_out", "commit_path_", "copy_pages_",
+def commit_paths_(cache_k, cache_v, draft_k, draft_v, requests, path_nodes, dest_pages,
+                  dest_slots):
+    """Commit the accepted nodes of several requests in one launch: entry i
+    writes draft[requests[i], path_nodes[i]] to (dest_pages[i], dest_slots[i])."""
+    return torch.ops.branchcraft.commit_paths_(
+        cache_k, cache_v, draft_k, draft_v, requests, path_nodes, dest_pages, dest_slots)
+
+
+__all__ = ["tree_verify", "packed_decode_out", "commit_path_", "copy_pages_", "commit_paths_",
            "LIBRARY_PATH"]

@@ -8,13 +8,16 @@ a commit of an accepted root-to-leaf path.  The bookkeeping lives in
 :class:`~branchcraft_torch.pages.PageOwner`; the device work -- the clone of
 a shared partial page and the accepted-path copy -- runs as the
 ``copy_pages_`` and ``commit_path_`` HIP ops on the current stream.
+``commit_many`` commits several requests with two launches in all (every
+clone, then every accepted node) and leaves the same pages and page tables
+as committing them one by one in the same order.
 """
 
 from __future__ import annotations
 
 import torch
 
-from . import commit_path_, copy_pages_, tree_verify
+from . import commit_path_, commit_paths_, copy_pages_, tree_verify
 from .pages import CommitPlan, PageOwner, Snapshot
 
 __all__ = ["PagedTreeCache", "Snapshot", "CommitPlan"]
@@ -105,3 +108,51 @@ class PagedTreeCache:
                      torch.tensor(plan.dest_pages, device=dev, dtype=torch.int32),
                      torch.tensor(plan.dest_slots, device=dev, dtype=torch.int32), 0)
         return plan
+
+    def commit_many(self, requests: list[int], paths: list[list[int]],
+                    draft_k: torch.Tensor, draft_v: torch.Tensor) -> list[CommitPlan]:
+        """Commit ``paths[i]`` of request ``requests[i]`` from ``draft_k[i]``.
+
+        Plans are made in list order, as consecutive ``commit`` calls would
+        make them.  All clones run first, then all accepted nodes: a page a
+        clone reads is shared, so no commit in the batch writes it, and every
+        commit target is either a fresh page or one its request owns alone.
+        If the pool runs out part way, the plans made so far are still
+        executed before the error is raised."""
+        if len(requests) != len(paths) or len(set(requests)) != len(requests):
+            raise ValueError("requests must be distinct and match paths")
+        if draft_k.shape != draft_v.shape or draft_k.shape[0] != len(requests):
+            raise ValueError("draft K/V must match and have one row per request")
+        nodes = draft_k.shape[1]
+        for path in paths:
+            if not path or len(path) > nodes:
+                raise ValueError("path is empty or longer than draft")
+            if any(node < 0 or node >= nodes for node in path):
+                raise ValueError("path node out of range")
+        plans: list[CommitPlan] = []
+        error = None
+        for request, path in zip(requests, paths):
+            try:
+                plans.append(self.owner.plan_commit(request, len(path)))
+            except RuntimeError as exc:  # pool exhausted: run what was planned
+                error = exc
+                break
+        self._run_plans(plans, paths, draft_k, draft_v)
+        if error is not None:
+            raise error
+        return plans
+
+    def _run_plans(self, plans, paths, draft_k, draft_v) -> None:
+        if not plans:
+            return
+        cows = [p.cow for p in plans if p.cow is not None]
+        rows = [(i, node, page, slot) for i, (p, path) in enumerate(zip(plans, paths))
+                for node, page, slot in zip(path, p.dest_pages, p.dest_slots)]
+        flat = [x for c in cows for x in c] + [x for r in rows for x in r]
+        idx = torch.tensor(flat, dtype=torch.int32).to(self.k.device)
+        if cows:
+            pairs = idx[:2 * len(cows)].view(-1, 2)
+            copy_pages_(self.k, self.v, pairs[:, 0].contiguous(), pairs[:, 1].contiguous())
+        table = idx[2 * len(cows):].view(-1, 4)
+        commit_paths_(self.k, self.v, draft_k, draft_v, *(table[:, j].contiguous()
+                                                          for j in range(4)))

@@ -130,6 +130,20 @@ int bc_commit_path(bc_shape shape, const bc_half* draft_k,
                    const int32_t* dest_slots, int request, int nodes,
                    int accepted, bc_stream_t stream);
 
+/* Accepted-path commits of several requests in one launch: entry i copies
+ * the K and V rows (all heads) of draft[requests[i], path_nodes[i]] into
+ * cache[dest_pages[i], dest_slots[i]], for i < count.  Drafts are
+ * [shape.batch, nodes, Hkv, D]; entries with a request, node, page or slot
+ * out of range are skipped.  No reference counterpart: it batches the
+ * per-request commit_path calls of a transaction (src/tree_attention.cu:
+ * 107-122; python/branchcraft_torch/transaction.py:144-148) into one launch.
+ * Entries must not write the same (page, slot) twice. */
+int bc_commit_paths(bc_shape shape, const bc_half* draft_k,
+                    const bc_half* draft_v, bc_half* cache_k, bc_half* cache_v,
+                    const int32_t* requests, const int32_t* path_nodes,
+                    const int32_t* dest_pages, const int32_t* dest_slots,
+                    int nodes, int count, bc_stream_t stream);
+
 /* Copy whole pages (all 16 slots, K and V) cache[dst_pages[i]] <-
  * cache[src_pages[i]] for i < count: the copy-on-write clone of a shared
  * partial page.  Out-of-range page ids are skipped.  No reference C++

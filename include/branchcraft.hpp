@@ -58,6 +58,17 @@ inline hipError_t commit_path(Shape shape, const half_bits* draft_k,
                                                 nodes, accepted, to_bc(stream)));
 }
 
+// Several requests' accepted nodes in one launch (no reference counterpart).
+inline hipError_t commit_paths(Shape shape, const half_bits* draft_k,
+                               const half_bits* draft_v, half_bits* cache_k,
+                               half_bits* cache_v, const int* requests, const int* path_nodes,
+                               const int* dest_pages, const int* dest_slots, int nodes,
+                               int count, hipStream_t stream = nullptr) {
+  return static_cast<hipError_t>(bc_commit_paths(shape, draft_k, draft_v, cache_k, cache_v,
+                                                 requests, path_nodes, dest_pages, dest_slots,
+                                                 nodes, count, to_bc(stream)));
+}
+
 inline hipError_t copy_pages(Shape shape, half_bits* cache_k, half_bits* cache_v,
                              const int* src_pages, const int* dst_pages, int count,
                              hipStream_t stream = nullptr) {

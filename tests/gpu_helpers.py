@@ -115,6 +115,19 @@ def commit(cache_k: torch.Tensor, cache_v: torch.Tensor, dk: torch.Tensor,
     torch.cuda.synchronize()
 
 
+def commit_paths(cache_k: torch.Tensor, cache_v: torch.Tensor, dk: torch.Tensor,
+                 dv: torch.Tensor, requests, nodes, dest_pages, dest_slots):
+    b, n, hkv, d = dk.shape
+    tr, tn, tdp, tds = (torch.tensor(x, device="cuda", dtype=torch.int32)
+                        for x in (requests, nodes, dest_pages, dest_slots))
+    shape = capi.Shape(b, hkv, hkv, d, 1, cache_k.shape[0])
+    check(lib().bc_commit_paths(shape, dk.data_ptr(), dv.data_ptr(), cache_k.data_ptr(),
+                                cache_v.data_ptr(), tr.data_ptr(), tn.data_ptr(),
+                                tdp.data_ptr(), tds.data_ptr(), n, len(requests), stream()),
+          "bc_commit_paths")
+    torch.cuda.synchronize()
+
+
 def copy_pages(cache_k: torch.Tensor, cache_v: torch.Tensor, src, dst):
     _, _, hkv, d = cache_k.shape
     ts = torch.tensor(src, device="cuda", dtype=torch.int32)

@@ -112,6 +112,21 @@ def test_commit_rejects(request_, nodes, accepted):
                               FAKE, FAKE, 0, 7, 1, None) == INVALID
 
 
+def test_commit_paths_rejects():
+    lib = capi.load()
+    s = capi.Shape(2, 8, 8, 128, 1, 16)
+    args = [FAKE] * 8
+    for i in range(8):  # every pointer is required
+        bad = list(args)
+        bad[i] = None
+        assert lib.bc_commit_paths(s, *bad, 7, 1, None) == INVALID
+    assert lib.bc_commit_paths(s, *args, 0, 1, None) == INVALID       # nodes < 1
+    assert lib.bc_commit_paths(s, *args, 7, -1, None) == INVALID      # count < 0
+    assert lib.bc_commit_paths(capi.Shape(0, 8, 8, 128, 1, 16), *args, 7, 1, None) == INVALID
+    assert lib.bc_commit_paths(capi.Shape(2, 8, 8, 96, 1, 16), *args, 7, 1, None) == INVALID
+    assert lib.bc_commit_paths(s, *args, 7, 0, None) == capi.BC_SUCCESS
+
+
 def test_copy_pages_rejects():
     lib = capi.load()
     s = capi.Shape(1, 8, 8, 128, 1, 16)
@@ -190,6 +205,10 @@ def test_torch_ops_register_reference_schemas():
     }
     for name, schema in want.items():
         assert str(getattr(torch.ops.branchcraft, name).default._schema) == schema
+    # added ops: the page clone and the batched commit
+    assert "commit_paths_(Tensor(a!) cache_k, Tensor(b!) cache_v" in str(
+        torch.ops.branchcraft.commit_paths_.default._schema)
+    assert "copy_pages_(Tensor(a!) cache_k" in str(torch.ops.branchcraft.copy_pages_.default._schema)
 
 
 def test_ops_have_no_cpu_fallback():

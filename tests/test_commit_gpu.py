@@ -143,3 +143,76 @@ def test_config3_commit_bit_exact(oracle):
     assert np.array_equal(store.k.cpu().numpy().view(np.uint16), ref_k.view(np.uint16))
     assert np.array_equal(store.v.cpu().numpy().view(np.uint16), ref_v.view(np.uint16))
     store.owner.check_invariants()
+
+
+def test_commit_paths_equals_per_request_commits(oracle):
+    """bc_commit_paths (one launch for several requests, with skipped
+    out-of-range entries) against the oracle's per-request commits."""
+    rng = np.random.default_rng(77)
+    P, hkv, d, b, n = 20, 8, 64, 4, 9
+    ck = rng.standard_normal((P, 16, hkv, d)).astype(np.float16)
+    cv = rng.standard_normal((P, 16, hkv, d)).astype(np.float16)
+    dk = rng.standard_normal((b, n, hkv, d)).astype(np.float16)
+    dv = rng.standard_normal((b, n, hkv, d)).astype(np.float16)
+    reqs = [0, 0, 1, 3, 3, 3, 2, 5, 1]          # request 5 is out of range
+    nodes = [0, 4, 2, 8, 1, 0, 7, 0, 9]          # node 9 is out of range
+    dpg = [2, 2, 7, 11, 11, 12, 19, 3, 4]
+    dsl = [0, 1, 15, 4, 5, 6, 9, 2, 3]
+    tk, tv = G.dev(ck), G.dev(cv)
+    G.commit_paths(tk, tv, G.dev(dk), G.dev(dv), reqs, nodes, dpg, dsl)
+    ek, ev = ck, cv
+    for r, x, p, s_ in zip(reqs, nodes, dpg, dsl):
+        if r < b:
+            ek, ev = oracle.commit(ek, ev, dk, dv, [x], [p], [s_], r)
+    assert np.array_equal(tk.cpu().numpy().view(np.uint16), ek.view(np.uint16))
+    assert np.array_equal(tv.cpu().numpy().view(np.uint16), ev.view(np.uint16))
+
+
+def _shared_store(seed):
+    from branchcraft_torch.transaction import PagedTreeCache
+    rng = np.random.default_rng(seed)
+    hkv, d = 2, 64
+    store = PagedTreeCache(40, hkv, d)
+    pk = G.dev(rng.standard_normal((37, hkv, d)).astype(np.float16))
+    pv = G.dev(rng.standard_normal((37, hkv, d)).astype(np.float16))
+    root = store.new(pk, pv)
+    reqs = [root, store.fork(root), store.fork(root)]
+    other = store.new(pk[:16], pv[:16])  # full last page: no clone
+    return store, reqs + [other]
+
+
+def test_commit_many_matches_sequential_commits():
+    """Two launches for all requests leave the same pages, lengths and page
+    bytes as one commit per request in the same order (shared partial page
+    cloned by the first two requests, written in place by the last sharer,
+    appended to a full page for the fourth)."""
+    rng = np.random.default_rng(5)
+    paths = [[0, 3, 4], [0, 1], [0, 2, 5, 6, 8, 1, 7, 3, 4, 10, 11, 9], [0, 4]]
+    dk = G.dev(rng.standard_normal((4, 12, 2, 64)).astype(np.float16))
+    dv = G.dev(rng.standard_normal((4, 12, 2, 64)).astype(np.float16))
+    seq, reqs = _shared_store(3)
+    seq_plans = [seq.commit(r, p, dk[i:i + 1].contiguous(), dv[i:i + 1].contiguous())
+                 for i, (r, p) in enumerate(zip(reqs, paths))]
+    bat, reqs2 = _shared_store(3)
+    plans = bat.commit_many(reqs2, paths, dk, dv)
+    torch.cuda.synchronize()
+    assert [p.cow for p in plans] == [p.cow for p in seq_plans]
+    assert plans[0].cow is not None and plans[2].cow is None  # last sharer writes in place
+    assert bat.pages == seq.pages and bat.lengths == seq.lengths
+    assert bat.refcount == seq.refcount and bat.free == seq.free
+    assert torch.equal(bat.k.view(torch.int16), seq.k.view(torch.int16))
+    assert torch.equal(bat.v.view(torch.int16), seq.v.view(torch.int16))
+
+
+def test_commit_many_runs_planned_work_before_pool_error():
+    from branchcraft_torch.transaction import PagedTreeCache
+    store = PagedTreeCache(3, 2, 64)
+    pk = torch.randn(15, 2, 64, device="cuda", dtype=torch.float16)
+    a = store.new(pk, pk)
+    b = store.new(pk, pk)
+    dk = torch.randn(2, 20, 2, 64, device="cuda", dtype=torch.float16)
+    with pytest.raises(RuntimeError):
+        store.commit_many([a, b], [[0], list(range(20))], dk, dk)
+    torch.cuda.synchronize()
+    assert store.lengths[a] == 16 and store.lengths[b] == 15
+    assert torch.equal(store.k[store.pages[a][0], 15], dk[0, 0])

@@ -146,3 +146,20 @@ def test_op_argument_errors_raise():
         bc.tree_verify(q, pk, pv, pages, lengths, dk, dv, parent[:, :3])  # shape
     with pytest.raises(RuntimeError):
         bc.tree_verify(q.cpu(), pk, pv, pages, lengths, dk, dv, parent)  # device
+
+
+def test_commit_paths_op_and_opcheck():
+    cache_k = torch.zeros(5, 16, 2, 64, device="cuda", dtype=torch.float16)
+    cache_v = torch.zeros_like(cache_k)
+    draft_k = torch.randn(2, 3, 2, 64, device="cuda", dtype=torch.float16)
+    draft_v = torch.randn_like(draft_k)
+    i32 = dict(device="cuda", dtype=torch.int32)
+    args = (cache_k, cache_v, draft_k, draft_v, torch.tensor([0, 1, 1], **i32),
+            torch.tensor([2, 0, 1], **i32), torch.tensor([4, 1, 1], **i32),
+            torch.tensor([0, 7, 8], **i32))
+    bc.commit_paths_(*args)
+    assert torch.equal(cache_k[4, 0], draft_k[0, 2]) and torch.equal(cache_v[1, 8], draft_v[1, 1])
+    assert torch.equal(cache_k[1, 7], draft_k[1, 0])
+    assert torch.count_nonzero(cache_k[2:4]) == 0
+    torch.library.opcheck(torch.ops.branchcraft.commit_paths_, args,
+                          test_utils=("test_schema", "test_faketensor"))
