@@ -40,7 +40,7 @@ HBM_PEAK_GBS = 8000.0
 # HBM bytes per config-5 call measured with rocprofv3 counters: attention
 # FETCH 275,684.7 KiB x 2 + WRITE 5,028.8 KiB, merge FETCH 2,636.0 KiB x 2 +
 # WRITE 472.0 KiB (FETCH_SIZE reads half of a 512 MiB copy's bytes).
-C5_HBM_TRAFFIC_BYTES = (275684.7 * 2 + 5028.8 + 2636.0 * 2 + 472.0) * 1024
+C5_HBM_TRAFFIC_BYTES = (275585.2 * 2 + 5028.8 + 2640.5 * 2 + 472.0) * 1024
 MFMA_F16_PEAK_TFLOPS = 2500.0
 PAGE = 16
 
@@ -154,7 +154,7 @@ def bench_c1(cx):
     out = t.empty((1, 32, 128), device="cuda", dtype=t.float32)
     shape = cx.capi.Shape(1, 32, 8, 128, 32, 64)
     res = {}
-    for splits in (1, cx.lib.bc_auto_splits(shape, 512, cx.cus), 8):
+    for splits in sorted({1, cx.lib.bc_auto_splits(shape, 512, cx.cus), 8}):
         scr = decode_scratch(cx, 1, 32, 128, splits)
         us = median_us(t, make_decode_call(cx, q, k, v, tp, tl, out, splits, scr))
         res[f"splits{splits}_us"] = round(us, 3)
@@ -264,7 +264,8 @@ def tree_setup(cx, batch, prefix, seed):
         pages=t.from_numpy(pages).cuda(), parent_np=parent,
         parent=t.from_numpy(parent).cuda(),
         lengths=t.full((batch,), prefix, device="cuda", dtype=t.int32),
-        batch=batch, prefix=prefix, hq=hq, hkv=hkv, d=d, n=n, pool=pool, pages_np=pages)
+        batch=batch, prefix=prefix, hq=hq, hkv=hkv, d=d, n=n, pool=pool, pages_np=pages,
+        free_pages=[int(x) for x in perm[npg:]])
     f["out"] = t.empty((batch, n, hq, d), device="cuda", dtype=t.float32)
     return f
 
@@ -390,16 +391,20 @@ def bench_tree(cx, batch, prefix, seed, with_expanded):
 
 
 def bench_commit(cx, f):
-    """Config 3 commit: each request clones the shared partial page, then
-    writes a random root-to-leaf path.  Two launches, as
-    PagedTreeCache.commit_many issues them: every clone (bc_copy_pages), then
-    every accepted node of every request (bc_commit_paths)."""
+    """Commit after verification: each request writes a random root-to-leaf
+    path at the end of the shared prefix.  A prefix that ends inside a page
+    (config 3, 2,053 tokens) clones that shared page per request first; one
+    that fills its last page (config 2, 2,048 tokens) writes the path into a
+    fresh page.  The launches are the ones PagedTreeCache.commit_many issues:
+    every clone (bc_copy_pages), then every accepted node of every request
+    (bc_commit_paths)."""
     t = cx.torch
     capi = cx.capi
     rng = np.random.default_rng(303)
     b, n, hkv, d, L = f["batch"], f["n"], f["hkv"], f["d"], f["prefix"]
+    partial = L % PAGE != 0
     last = int(f["pages_np"][0, (L - 1) // PAGE])
-    fresh = list(range(f["pool"] - b, f["pool"]))
+    fresh = f["free_pages"][:b]
     src = t.tensor([last] * b, device="cuda", dtype=t.int32)
     dst = t.tensor(fresh, device="cuda", dtype=t.int32)
     shape = capi.Shape(b, hkv, hkv, d, 1, f["pool"])
@@ -411,17 +416,18 @@ def bench_commit(cx, f):
         path = ancestors(par, int(rng.choice(leaves)))[::-1]
         for j, node in enumerate(path):
             pos = L + j
-            page = fresh[bi] if pos // PAGE == (L - 1) // PAGE else -1
-            rows.append((bi, node, page, pos % PAGE))
-    if any(r[2] < 0 for r in rows):
-        raise RuntimeError("config 3 paths must fit the cloned partial page")
+            if pos // PAGE != L // PAGE:
+                raise RuntimeError("accepted path must fit the page that follows the prefix")
+            rows.append((bi, node, fresh[bi], pos % PAGE))
     reqs, nodes, pages, slots = (t.tensor([r[j] for r in rows], device="cuda", dtype=t.int32)
                                  for j in range(4))
     lib, st = cx.lib, cx.stream()
 
     def call():
-        err = lib.bc_copy_pages(shape, k.data_ptr(), v.data_ptr(), src.data_ptr(),
-                                dst.data_ptr(), b, st)
+        err = 0
+        if partial:
+            err |= lib.bc_copy_pages(shape, k.data_ptr(), v.data_ptr(), src.data_ptr(),
+                                     dst.data_ptr(), b, st)
         err |= lib.bc_commit_paths(shape, f["dk"].data_ptr(), f["dv"].data_ptr(),
                                    k.data_ptr(), v.data_ptr(), reqs.data_ptr(),
                                    nodes.data_ptr(), pages.data_ptr(), slots.data_ptr(),
@@ -429,8 +435,10 @@ def bench_commit(cx, f):
         if err:
             raise RuntimeError("commit failed")
     us = median_us(t, call)
-    moved = 2 * b * PAGE * hkv * d * 2 * 2 + 2 * len(rows) * hkv * d * 2 * 2
-    return {"us": round(us, 3), "bytes": moved, "launches": 2, "accepted_nodes": len(rows)}
+    cloned = b if partial else 0
+    moved = 2 * cloned * PAGE * hkv * d * 2 * 2 + 2 * len(rows) * hkv * d * 2 * 2
+    return {"us": round(us, 3), "bytes": moved, "launches": 2 if partial else 1,
+            "cloned_pages": cloned, "accepted_nodes": len(rows)}
 
 
 # ---------------------------------------------------------------------------

@@ -147,14 +147,18 @@ __global__ __launch_bounds__(kThreads, 2) void tree_kernel(TreeParams P) {
   __shared__ __attribute__((aligned(16))) char s_mem[kWaves * kTile * VP * 2];
   __shared__ float s_m[2][32], s_l[2][32];
   if (wave == 0) {
+    // Rows past the tile's query rows read row (node 0, head h) and store
+    // zeros; every load is issued before the first store.
     const uint16_t* qp = P.dq + (((size_t)b * P.nodes + node) * P.hq + h) * D + 8 * g;
+    uint4 qf[KS];
 #pragma unroll
-    for (int s = 0; s < KS; ++s) s_q[s][lane] = rvalid ? ldg16(qp + 16 * s) : make_uint4(0, 0, 0, 0);
+    for (int s = 0; s < KS; ++s) qf[s] = ldg16(qp + 16 * s);
+#pragma unroll
+    for (int s = 0; s < KS; ++s) s_q[s][lane] = rvalid ? qf[s] : make_uint4(0, 0, 0, 0);
   }
   if (drafts)
     for (int i = threadIdx.x; i < P.nodes; i += kThreads)
       s_parent[i] = P.parent[(size_t)b * P.nodes + i];
-  __syncthreads();
 
   _Float16* vs = reinterpret_cast<_Float16*>(s_mem) + wave * kTile * VP;
   // Transpose-read address of this lane: group G = lane/16, j = lane%16.
@@ -332,9 +336,14 @@ __global__ __launch_bounds__(kThreads, 2) void tree_kernel(TreeParams P) {
   bool ta = false, tb = false;
   bool pa[2] = {true, true}, pbk[2] = {true, true};
   int idb[2];
+  // The first tile's loads go out before the barrier that publishes Q and
+  // the parent array.
   if (nmine > 0) {
     issue(0, ida, ka, va, ta, pa);
     ids_of(1, idb);
+  }
+  __syncthreads();
+  if (nmine > 0) {
     for (int idx = 0; idx < nmine; idx += 2) {
       issue(idx + 1, idb, kb, vb, tb, pbk);
       ids_of(idx + 2, ida);
@@ -514,9 +523,12 @@ TreeParams make_params(const bc_shape& s, const bc_tree_inputs& in, int nodes) {
   return P;
 }
 
-// Prefix chunking for the workspace path: one workgroup per CU (the kernel
-// fits one per CU), counting the draft part of every unit, chunks of at
-// least 128 tokens, multiples of 32.
+// Prefix chunking for the workspace path: about one workgroup per CU,
+// counting the draft part of every unit, chunks of at least 128 tokens,
+// multiples of 32.  Two workgroups fit a CU, but halving the chunks to fill
+// both measured slower at 8 x 2053 tokens (22.7 against 20.9 us): each
+// workgroup's fixed start, merge and partial-write cost outweighs the
+// second wave per SIMD.
 void tree_chunking(const bc_shape& s, int nodes, int* chunk_tokens, int* parts) {
   const int group = s.query_heads / s.kv_heads;
   const long long units =
