@@ -292,12 +292,15 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == kMaxWaves ? 3 : 2) void paged_
 
   // Issue cursor: walks the same pages ahead of the compute cursor.  Page
   // ids are scalar loads (counted by lgkmcnt, not vmcnt), fetched one step
-  // before the K/V loads that use them; issues past the range repeat the
-  // last page (an L2 hit), so every path has the same loads in flight.
-  int ib = pb, ilocal = plocal, ipages = ppages, issued = 0, last_phys = 0;
+  // before the K/V loads that use them.  Issues past the range still load
+  // (every path keeps the same loads in flight), but from page 0 of the pool
+  // like an out-of-pool id: all of them share that one L2-resident page,
+  // whereas repeating the range's last page would fetch it from HBM again,
+  // since the page loads are non-temporal (about 25 MB per call at C5).
+  int ib = pb, ilocal = plocal, ipages = ppages, issued = 0;
   auto next_id = [&]() -> int {
-    if (issued >= count) return last_phys;
-    last_phys = P.pages[(size_t)ib * P.max_pages + ilocal];
+    if (issued >= count) return -1;
+    const int phys = P.pages[(size_t)ib * P.max_pages + ilocal];
     ++issued;
     if (++ilocal == ipages && issued < count) {
       do {
@@ -306,7 +309,7 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == kMaxWaves ? 3 : 2) void paged_
       } while (ipages == 0);
       ilocal = 0;
     }
-    return last_phys;
+    return phys;
   };
 
   auto issue = [&](int phys, uint4 (&kb)[KS], uint4 (&vb)[KS], bool& valid) {
@@ -673,8 +676,17 @@ extern "C" int bc_auto_splits(bc_shape s, int max_length, int cu_count) {
   return (int)splits;
 }
 
+// Packed decode splits the pages over flat ranges (workspace + merge) unless
+// the page table is short enough for the unsplit mode, by the same rule as
+// bc_auto_splits with the table's capacity as the context bound; the choice
+// needs only the shape, so callers never read lengths back to the host.
+static bool packed_split(const bc_shape& s) {
+  const long long cap = (long long)s.max_pages * BC_PAGE_SIZE;
+  return bc_auto_splits(s, cap > (1 << 30) ? (1 << 30) : (int)cap, device_cus()) > 1;
+}
+
 extern "C" size_t bc_packed_decode_workspace_size(bc_shape s) {
-  if (!shape_ok(s)) return 0;
+  if (!shape_ok(s) || !packed_split(s)) return 0;
   return packed_workspace(s, packed_nwg(s));
 }
 
@@ -704,7 +716,7 @@ static int packed_common(bc_shape s, const bc_half* q, const bc_half* kv,
   P.scale_log2 = (float)((double)scale * 1.4426950408889634);
   const int nwg = packed_nwg(s);
   const size_t need = packed_workspace(s, nwg);
-  if (ws && ws_bytes >= need) {
+  if (ws && ws_bytes >= need && packed_split(s)) {
     P.nwg = nwg;
     const size_t slots = (size_t)nwg + s.batch;
     const size_t acc_bytes =

@@ -168,13 +168,16 @@ int bc_packed_decode(bc_shape shape, const bc_half* q, const bc_half* packed_kv,
                      long long head_stride, long long slot_stride,
                      long long kv_stride, float scale, bc_stream_t stream);
 
-/* Bytes of workspace bc_packed_decode_ws needs for this shape. */
+/* Bytes of workspace bc_packed_decode_ws needs for this shape.  0 when the
+ * page table holds at most 1024 tokens (max_pages * 16) and one workgroup per
+ * (sequence, head block) fits the CUs: such calls run unsplit, with no merge,
+ * whatever workspace is passed (the bc_auto_splits rule, from the shape only). */
 size_t bc_packed_decode_workspace_size(bc_shape shape);
 
 /* bc_packed_decode with long sequences split into fixed token chunks across
  * workgroups and an FP32 merge; chunking depends on shape.max_pages only,
  * so no device lengths are read on the host.  A null or undersized
- * workspace falls back to bc_packed_decode. */
+ * workspace, or a shape whose workspace size is 0, runs bc_packed_decode. */
 int bc_packed_decode_ws(bc_shape shape, const bc_half* q,
                         const bc_half* packed_kv, const int32_t* pages,
                         const int32_t* lengths, bc_half* output,

@@ -178,9 +178,13 @@ def test_workspace_sizes():
     lib = capi.load()
     c5 = capi.Shape(64, 32, 8, 128, 256, 20000)
     assert lib.bc_packed_decode_workspace_size(c5) > 0
-    # flat page ranges are used whatever the context length
-    assert lib.bc_packed_decode_workspace_size(capi.Shape(4, 32, 8, 128, 8, 64)) > 0
-    assert lib.bc_packed_decode_workspace_size(capi.Shape(4, 32, 8, 96, 8, 64)) == 0
+    # Page tables of at most 1024 tokens whose (sequence, head block)
+    # workgroups fit the CUs run unsplit: no workspace.
+    assert lib.bc_packed_decode_workspace_size(capi.Shape(4, 32, 8, 128, 8, 64)) == 0
+    assert lib.bc_packed_decode_workspace_size(capi.Shape(4, 32, 8, 128, 64, 64)) == 0
+    assert lib.bc_packed_decode_workspace_size(capi.Shape(4, 32, 8, 128, 65, 64)) > 0
+    assert lib.bc_packed_decode_workspace_size(capi.Shape(64, 32, 8, 128, 8, 64)) > 0
+    assert lib.bc_packed_decode_workspace_size(capi.Shape(4, 32, 8, 96, 80, 64)) == 0
     c3 = capi.Shape(8, 32, 8, 128, 129, 160)
     assert lib.bc_tree_verify_workspace_size(c3, 7) > 0
     assert lib.bc_tree_verify_workspace_size(c3, 0) == 0

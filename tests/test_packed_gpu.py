@@ -13,6 +13,7 @@ import pytest
 import torch
 
 from oracle import oracle_np
+import branchcraft_capi as capi
 import gpu_helpers as G
 
 pytestmark = pytest.mark.gpu
@@ -21,12 +22,23 @@ pytestmark = pytest.mark.gpu
 def _run_both(q, cache, strides, hkv, phys, pages, lengths, scale, oracle, atol=2e-3):
     exp32, _ = oracle.packed_decode(q, cache.cpu().numpy(), pages, lengths, strides, hkv,
                                     scale)
-    for ws in (False, True):
-        out = G.packed(q, cache, strides, hkv, phys, pages, lengths, scale, workspace=ws)
+    # The same inputs again through a page table of 80 columns: more than 1024
+    # tokens of capacity take the split path (flat page ranges and the merge)
+    # where a short table runs unsplit.
+    wide = np.full((pages.shape[0], max(pages.shape[1], 80)), -1, dtype=np.int32)
+    wide[:, :pages.shape[1]] = pages
+    b, hq, d = q.shape
+    if G.lib().bc_packed_decode_workspace_size(capi.Shape(b, hq, hkv, d, 80, phys)) > 0:
+        runs = ((False, pages), (True, pages), (True, wide))
+    else:  # batches large enough that the split rule keeps even 1280 tokens unsplit
+        runs = ((False, pages), (True, pages))
+    for ws, pg in runs:
+        out = G.packed(q, cache, strides, hkv, phys, pg, lengths, scale, workspace=ws)
         tol = G.f16_tolerance(exp32, atol)
         err = np.abs(out.astype(np.float32) - exp32)
         assert np.all(np.isfinite(out)), "non-finite output"
-        assert np.all(err <= tol), f"workspace={ws}: max err {err.max():.3e}"
+        assert np.all(err <= tol), (f"workspace={ws} columns={pg.shape[1]}: "
+                                    f"max err {err.max():.3e}")
     return exp32
 
 
