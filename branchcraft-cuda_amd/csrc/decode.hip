@@ -105,14 +105,6 @@ __device__ void flat_geometry(const AttnParams& P, int lane, int& total, int& pe
   per = (t + P.nwg - 1) / P.nwg;
 }
 
-// Pages of the sequences before b.
-__device__ int pages_before(const AttnParams& P, int lane, int b) {
-  int t = 0;
-  for (int base = 0; base < b; base += 64)
-    t += wave_sum_i(base + lane < b ? seq_pages(P, base + lane) : 0);
-  return t;
-}
-
 // Sequence holding flat page f (f < total) and the flat index of its first page.
 __device__ void locate(const AttnParams& P, int lane, int f, int& b, int& start) {
   int run = 0;
@@ -473,9 +465,10 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == kMaxWaves ? 3 : 2) void paged_
 
 // Flat mode: out = sum_w 2^(m_w - M) a_w / sum_w 2^(m_w - M) l_w over the
 // workgroups whose ranges cut sequence b (src/paged_gqa.cu:76-106); empty
-// sequences give zeros.  One wave per (b, h) output row: lane i reads
-// partial i's (max, sum), the weights are formed once, then every lane
-// accumulates its dims over the partials with independent loads.
+// sequences give zeros.  One wave per (b, h) output row, two dependent
+// memory rounds: the lengths (page geometry), then every partial's (max,
+// sum) together with the first eight partials' accumulators; lane i holds
+// partial i's weight and every lane accumulates its dims.
 template <int D, typename OutT>
 __global__ __launch_bounds__(256) void merge_kernel(AttnParams P) {
   constexpr int PER = D / 64;
@@ -483,48 +476,64 @@ __global__ __launch_bounds__(256) void merge_kernel(AttnParams P) {
   const int rowi = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (rowi >= P.batch * P.hq) return;
   const int b = rowi / P.hq, h = rowi % P.hq;
-  const int np = seq_pages(P, b);
+  // One round of length loads: the batch's page total (as flat_geometry),
+  // the pages before sequence b and b's own page count.
+  int total = 0, before = 0, np = 0;
+  for (int base = 0; base < P.batch; base += 64) {
+    const int i = base + lane;
+    const int n = i < P.batch ? seq_pages(P, i) : 0;
+    total += wave_sum_i(n);
+    before += wave_sum_i(i < b ? n : 0);
+    if (b >= base && b < base + 64) np = __builtin_amdgcn_readlane(n, b - base);
+  }
   if (np == 0) {
 #pragma unroll
     for (int j = 0; j < PER; ++j) store_out<OutT>(P.out, (size_t)rowi * D + lane + 64 * j, 0.f);
     return;
   }
-  int total, per;
-  flat_geometry(P, lane, total, per);
-  const int start = pages_before(P, lane, b);
-  const int w0 = start / per, w1 = (start + np - 1) / per;
+  const int per = (total + P.nwg - 1) / P.nwg;
+  const int w0 = before / per, w1 = (before + np - 1) / per;
   if (w0 == w1) return;  // the sequence ended inside one range: written directly
   float mm = kNegInf, lsum = 0.f, a[PER];
 #pragma unroll
   for (int j = 0; j < PER; ++j) a[j] = 0.f;
+  // Eight partials per step, all loads issued before the first use; parts
+  // past cnt re-read the last valid partial (finite) with weight 0.
+  auto load8p = [&](int wb, int cnt, int i0, float (&v)[8][PER]) {
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int i = min(i0 + u, cnt - 1);
+      const float* src = P.part_acc + ((size_t)(wb + i + b) * P.hq + h) * D + lane;
+#pragma unroll
+      for (int j = 0; j < PER; ++j) v[u][j] = src[64 * j];
+    }
+  };
   for (int wb = w0; wb <= w1; wb += 64) {
     const int cnt = min(64, w1 - wb + 1);
-    float mp = kNegInf, lp = 0.f;
-    if (lane < cnt) {
-      const size_t r = (size_t)(wb + lane + b) * P.hq + h;
-      mp = P.part_ml[2 * r];
-      lp = P.part_ml[2 * r + 1];
-    }
-    const float bmax = wave_max(mp);
-    if (bmax == kNegInf) continue;
-    const float mn = __builtin_fmaxf(mm, bmax);
-    const float a1 = fast_exp2(mm - mn);
-    const float w = fast_exp2(mp - mn);  // 0 for empty partials
+    // The (max, sum) loads and the first step's partials go out together:
+    // the partial loads do not depend on the weights.
+    const size_t r = (size_t)(wb + min(lane, cnt - 1) + b) * P.hq + h;
+    const float mp0 = P.part_ml[2 * r], lp0 = P.part_ml[2 * r + 1];
+    float v[8][PER];
+    load8p(wb, cnt, 0, v);
+    // One wait for both load sets here; left alone, the compiler sinks the
+    // partial loads below the reductions and pays a second round trip.
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+#pragma unroll
+      for (int j = 0; j < PER; ++j) asm volatile("" ::"v"(v[u][j]));
+    const float mp = lane < cnt ? mp0 : kNegInf;
+    const float lp = lane < cnt ? lp0 : 0.f;
+    const float mn = __builtin_fmaxf(mm, wave_max(mp));
+    const float ms = safe_max(mn);   // all-empty so far: every weight is 0
+    const float a1 = fast_exp2(mm - ms);
+    const float w = fast_exp2(mp - ms);  // 0 for empty partials
     lsum = lsum * a1 + wave_sum(w * lp);
 #pragma unroll
     for (int j = 0; j < PER; ++j) a[j] *= a1;
     mm = mn;
-    // Eight partials per step, all loads issued before the first use.  Parts
-    // past cnt re-read the last valid partial (finite) with weight 0.
     for (int i0 = 0; i0 < cnt; i0 += 8) {
-      float v[8][PER];
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const int i = min(i0 + u, cnt - 1);
-        const float* src = P.part_acc + ((size_t)(wb + i + b) * P.hq + h) * D + lane;
-#pragma unroll
-        for (int j = 0; j < PER; ++j) v[u][j] = src[64 * j];
-      }
+      if (i0 > 0) load8p(wb, cnt, i0, v);
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
         const float wi = __builtin_bit_cast(

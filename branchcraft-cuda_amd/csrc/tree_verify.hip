@@ -451,27 +451,38 @@ __global__ __launch_bounds__(256) void merge_tree_kernel(TreeParams P) {
   const size_t base = row * (P.prefix_parts + 1);
   // slot of part i: prefix chunks 0..nparts-1, then the draft slot
   auto slot = [&](int i) { return base + (i == nparts ? P.prefix_parts : i); };
-  float mp = kNegInf, lp = 0.f;
-  if (lane <= nparts) {  // nparts < 64 is guaranteed by tree_chunking
-    mp = P.part_ml[2 * slot(lane)];
-    lp = P.part_ml[2 * slot(lane) + 1];
-  }
-  const float mm = wave_max(mp);
-  const float w = fast_exp2(mp - mm);  // every row sees its own node: mm finite
-  const float lsum = wave_sum(w * lp);
-  float a[PER];
-#pragma unroll
-  for (int j = 0; j < PER; ++j) a[j] = 0.f;
   // Eight parts per step, all loads issued before the first use; steps past
   // the last part re-read it with weight 0 (lanes past nparts hold w = 0).
-  for (int i0 = 0; i0 <= nparts; i0 += 8) {
-    float v[8][PER];
+  auto load8p = [&](int i0, float (&v)[8][PER]) {
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
       const float* src = P.part_acc + slot(min(i0 + u, nparts)) * D + lane;
 #pragma unroll
       for (int j = 0; j < PER; ++j) v[u][j] = src[64 * j];
     }
+  };
+  // Every part's (max, sum) (nparts < 64 is guaranteed by tree_chunking) and
+  // the first eight parts' accumulators go out together, one wait for both:
+  // left alone, the compiler sinks the accumulator loads below the
+  // reductions and pays a second round trip.
+  const size_t ms = slot(min(lane, nparts));
+  const float mp0 = P.part_ml[2 * ms], lp0 = P.part_ml[2 * ms + 1];
+  float v[8][PER];
+  load8p(0, v);
+#pragma unroll
+  for (int u = 0; u < 8; ++u)
+#pragma unroll
+    for (int j = 0; j < PER; ++j) asm volatile("" ::"v"(v[u][j]));
+  const float mp = lane <= nparts ? mp0 : kNegInf;
+  const float lp = lane <= nparts ? lp0 : 0.f;
+  const float mm = wave_max(mp);
+  const float w = fast_exp2(mp - mm);  // every row sees its own node: mm finite
+  const float lsum = wave_sum(w * lp);
+  float a[PER];
+#pragma unroll
+  for (int j = 0; j < PER; ++j) a[j] = 0.f;
+  for (int i0 = 0; i0 <= nparts; i0 += 8) {
+    if (i0 > 0) load8p(i0, v);
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
       const float wi = __builtin_bit_cast(
