@@ -314,17 +314,28 @@ __global__ __launch_bounds__(kThreads, 2) void tree_kernel(TreeParams P) {
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     // ---- O^T += V^T P^T; A operand tokens 16st + 8hf + 4g + k, dim lr ----
+    // The MFMAs go round the DT accumulators, so consecutive ones are
+    // independent: one accumulator's chain of four would wait out each
+    // MFMA's latency in turn.
+    f16x8 av[DT][2];
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt) {
+    for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
       for (int st = 0; st < 2; ++st) {
         const f16x4 lo = lds_read_tr(vtr + (16 * st) * VP + 32 * dt);
         const f16x4 hi = lds_read_tr(vtr + (16 * st + 8) * VP + 32 * dt);
-        const f16x8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-        acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pb[st], acc[dt], 0, 0, 0);
-        acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pl[st], acc[dt], 0, 0, 0);
+        av[dt][st] = f16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
       }
-    }
+#pragma unroll
+    for (int st = 0; st < 2; ++st)
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+        acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[dt][st], pb[st], acc[dt], 0, 0, 0);
+#pragma unroll
+    for (int st = 0; st < 2; ++st)
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+        acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[dt][st], pl[st], acc[dt], 0, 0, 0);
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
