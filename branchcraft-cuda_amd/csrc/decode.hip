@@ -105,6 +105,22 @@ __device__ void flat_geometry(const AttnParams& P, int lane, int& total, int& pe
   per = (t + P.nwg - 1) / P.nwg;
 }
 
+// The sequence with the rank-th most pages (ties by index).  Workgroups are
+// dispatched in index order, so giving the lowest indices the longest
+// sequences balances the rounds of one-workgroup-per-sequence launches.
+// Single sequences and batches above 64 sequences keep index order.
+__device__ int seq_by_rank(const AttnParams& P, int lane, int rank) {
+  if (P.batch == 1 || P.batch > 64) return rank;
+  const int n = lane < P.batch ? seq_pages(P, lane) : -1;
+  int r = 0;
+  for (int k = 0; k < P.batch; ++k) {
+    const int nk = __builtin_amdgcn_readlane(n, k);
+    r += (nk > n || (nk == n && k < lane)) ? 1 : 0;
+  }
+  const unsigned long long hit = __builtin_amdgcn_ballot_w64(lane < P.batch && r == rank);
+  return __builtin_ffsll((long long)hit) - 1;
+}
+
 // Sequence holding flat page f (f < total) and the flat index of its first page.
 __device__ void locate(const AttnParams& P, int lane, int f, int& b, int& start) {
   int run = 0;
@@ -209,7 +225,7 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == kMaxWaves ? 3 : 2) void paged_
   // pages in all (crossing into later sequences in flat mode).
   int pb, plocal, count;
   if (sliced) {
-    pb = rid;
+    pb = seq_by_rank(P, lane, rid);
     const int np = seq_pages(P, pb);
     plocal = wave * np / WAVES;
     count = (wave + 1) * np / WAVES - plocal;  // may be 0 (an empty slice)
