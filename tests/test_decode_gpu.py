@@ -102,3 +102,19 @@ def test_head_layouts_beyond_reference(hq, hkv, d, oracle):
     for splits in (1, 3, 40):
         out = G.decode(q, k, v, pages, lengths, splits)
         G.gate(out, expected, 3e-4, f"Hq={hq} Hkv={hkv} D={d} splits={splits}")
+
+
+@pytest.mark.parametrize("batch", [40, 64, 70])
+def test_unsplit_ragged_batches(batch, oracle):
+    """splits = 1 runs one workgroup per (sequence, head block), and
+    workgroup r takes the sequence with the r-th most pages (ties by index)
+    for batches of up to 64; larger batches keep index order.  Ragged
+    lengths with ties and empty sequences cover both orders."""
+    rng = np.random.default_rng(batch)
+    lens = rng.integers(0, 300, size=batch)
+    lens[::7] = 129
+    lens[3] = 0
+    q, k, v, pages, lengths = oracle_np.paged_fixture(rng, batch, 8, 2, 64, list(lens))
+    expected = oracle.decode(q, k, v, pages, lengths, threads=8)
+    G.gate(G.decode(q, k, v, pages, lengths, 1), expected, 3e-4, f"B={batch} splits=1")
+    G.gate(G.decode(q, k, v, pages, lengths, 5), expected, 3e-4, f"B={batch} splits=5")
