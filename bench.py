@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the Branchcraft paged-attention hot path on one MI355X.
 
-Headline (`value`): BASELINE config 5 -- packed-KV decode, batch 64, ragged
+Headline (`value`): benchmark config 5 -- packed-KV decode, batch 64, ragged
 contexts U[128, 4096], 32/8 heads, D=128, cache [20000, 2, 16, 8, 128] FP16
 -- as algorithmic HBM GB/s (each attended token's K+V once, plus Q, output,
 used page-table entries and lengths) over one call of bc_packed_decode_ws
@@ -557,7 +557,7 @@ def main():
         "dtype": "f16",
         "data": "synthetic (seeded N(0,1) FP16 K/V/Q, random block tables)",
         "config": {
-            "workload": ("BASELINE config 5: packed-KV decode, batch 64, contexts "
+            "workload": ("benchmark config 5: packed-KV decode, batch 64, contexts "
                          "U[128,4096], 32 Q / 8 KV heads, D=128, cache [20000,2,16,8,128] "
                          "FP16, FP16 output"),
             "decode_us_per_call": round(ms * 1e3, 3),

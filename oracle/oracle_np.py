@@ -6,7 +6,7 @@ operations, without the C oracle's float casts or token loop, and derive
 ancestor sets by brute force.  They follow the reference's torch oracles
 (tests/test_torch_ops.py:32-52 and :77-88 of Haaziq386/branchcraft-cuda).
 
-Fixture generators produce the BASELINE configurations' shapes from a
+Fixture generators produce the benchmark configurations' shapes from a
 numpy seed (inputs are stored with the golden files, so generation never
 has to be reproduced bit for bit across numpy versions).
 """
@@ -122,7 +122,7 @@ def paged_fixture(rng, batch, hq, hkv, d, lengths, spare=7, sigma=0.5, pool=None
 
 
 def random_parents(rng, batch, nodes):
-    """parent[0] = -1, parent[i] ~ U{0..i-1}."""
+    """parent[0] = -1, parent[i] ~ U{0..i-1} (benchmark configs 2-3)."""
     par = np.full((batch, nodes), -1, dtype=np.int32)
     for bi in range(batch):
         for i in range(1, nodes):

@@ -4,7 +4,7 @@
 // Restates the reference driver (src/main.cu of Haaziq386/branchcraft-cuda):
 // the same test cases and 3e-4 gates (:252-352), the same benchmark sweeps,
 // timing protocol (5 warm-ups, 7 trials x 20 launches, median; :354-373) and
-// CSV columns (:451-453, :495-496), plus `config N` for the five BASELINE
+// CSV columns (:451-453, :495-496), plus `config N` for the five benchmark
 // configurations with the CPU oracle timed on this host.  Kernels are reached
 // only through the C ABI (include/branchcraft.hpp); the HIP runtime is used
 // for device memory and events.  This is test and measurement tooling: it
@@ -520,7 +520,7 @@ void run_tree_bench(const std::string& path, bool quick) {
   std::cout << "Wrote " << path << '\n';
 }
 
-// ---- config N: the BASELINE configurations ---------------------------------------------
+// ---- config N: the benchmark configurations ---------------------------------------------
 
 template <typename F>
 double cpu_seconds(F&& f) {

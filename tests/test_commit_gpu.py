@@ -3,7 +3,7 @@
 Restates the reference's known-answer commit test
 (tests/test_torch_ops.py:99-114), its transaction test
 (tests/test_transaction.py:8-29) and the driver's commit / sibling /
-rollback case (src/main.cu:264-313), and runs BASELINE config 3's commit.
+rollback case (src/main.cu:264-313), and runs benchmark config 3's commit.
 """
 
 import numpy as np
@@ -110,7 +110,7 @@ def test_transaction_shared_partial_page_then_rollback():
 
 
 def test_config3_commit_bit_exact(oracle):
-    """8 requests share a 2053-token prefix (last page
+    """benchmark config 3: 8 requests share a 2053-token prefix (last page
     holds 5 tokens); each commits a random root-to-leaf path; every request
     clones the shared partial page."""
     from branchcraft_torch.transaction import PagedTreeCache

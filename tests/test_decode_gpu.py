@@ -3,7 +3,7 @@
 Cases restate the reference driver's suite (src/main.cu:318-352): empty,
 single token, page boundary 16/17, ragged batch, non-power-of-two GQA
 (10/2, 12/3), D=64/128 and splits 1..16 at its 3e-4 gate; then splits
-beyond the reference's cap, BASELINE config 1 and config 4 at full size.
+beyond the reference's cap, benchmark config 1 and config 4 at full size.
 """
 
 import numpy as np
@@ -32,7 +32,7 @@ def test_reference_cases_all_splits(case, oracle):
 
 
 def test_config1_b1_l512(oracle):
-    """B=1, L=512, 32/8 heads, D=128, pool of 64 pages,
+    """benchmark config 1: B=1, L=512, 32/8 heads, D=128, pool of 64 pages,
     page table = first 32 ids of a seeded permutation, N(0,1)."""
     rng = np.random.default_rng(1)
     perm = rng.permutation(64).astype(np.int32)
@@ -49,7 +49,7 @@ def test_config1_b1_l512(oracle):
 
 
 def test_config4_split_k_long_context(oracle):
-    """B=4, L ~ U[16384, 32768], random page map; the
+    """benchmark config 4: B=4, L ~ U[16384, 32768], random page map; the
     split count keeps chunks in [256, 2048] tokens."""
     rng = np.random.default_rng(4)
     lens = rng.integers(16384, 32769, size=4)

@@ -2,7 +2,7 @@
 
 Restates the reference's packed test (tests/test_torch_ops.py:62-96: HND and
 NHD strides, lengths [23, 9, 0]) and adds the [P,2,16,Hkv,D] layout of
-BASELINE config 5, unaligned strides, the split/unsplit paths and config 5
+benchmark config 5, unaligned strides, the split/unsplit paths and config 5
 at full size.  FP16 outputs are gated at 2e-3 plus half an FP16 ulp.
 """
 
@@ -69,7 +69,7 @@ def test_reference_packed_layouts(layout, dim, oracle):
 
 def test_five_dim_layout_small(oracle):
     """[P, 2, 16, Hkv, D]: K at block*16*2*Hkv*D + slot*Hkv*D + head*D, V at
-    +16*Hkv*D (BASELINE config 5's layout) at a small size."""
+    +16*Hkv*D (benchmark config 5's layout) at a small size."""
     rng = np.random.default_rng(3)
     P, hkv, d, hq, b = 40, 8, 128, 32, 5
     cache = torch.from_numpy(rng.standard_normal((P, 2, 16, hkv, d)).astype(np.float16)).cuda()
@@ -101,7 +101,7 @@ def test_unaligned_strides_take_the_scalar_path(oracle):
 
 
 def test_config5_full_size(oracle):
-    """B=64, contexts U[128, 4096], cache [20000,2,16,8,128],
+    """benchmark config 5: B=64, contexts U[128, 4096], cache [20000,2,16,8,128],
     block-table rows = consecutive slices of a seeded permutation."""
     rng = np.random.default_rng(5)
     B, hq, hkv, d, NB, maxp = 64, 32, 8, 128, 20000, 256

@@ -2,7 +2,7 @@
 
 Restates the reference driver's tree cases (src/main.cu:252-262: prefix
 {0, 17, 257}, B=2, N=7, binary parents, 3e-4), the reference torch test
-(tests/test_torch_ops.py:16-53), BASELINE configs 2 and 3, deep/wide trees
+(tests/test_torch_ops.py:16-53), benchmark configs 2 and 3, deep/wide trees
 over several MFMA row and draft tiles, and the invariant that the tree
 output equals paged decode over the expanded-prefix fixture
 (src/main.cu:375-423, 457-463).
