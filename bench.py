@@ -13,7 +13,8 @@ warm-ups, 7 trials x 20 launches, median; src/main.cu:354-373):
   C1 paged decode B=1 L=512;  C2 tree_verify 1 x 2048 + 7 nodes;
   C3 tree_verify 8 x (2048+5) shared prefix vs the expanded-prefix decode,
      plus the copy-on-write commit;  C4 split-K decode B=4, L~U[16K, 32K];
-  C5 packed decode without the workspace (single partition per sequence).
+  C5 packed decode without the workspace (single partition per sequence),
+     and 20 calls captured in one HIP graph and replayed (per-call time).
 The CPU baseline times the C oracle (oracle/bc_oracle.c) on the whole C5
 workload on this host's cores.
 
@@ -78,6 +79,37 @@ def median_us(torch, fn, trials=7, repeats=20, warmup=5):
         stop.record()
         stop.synchronize()
         times.append(start.elapsed_time(stop) * 1000.0 / repeats)
+    return statistics.median(times)
+
+
+def graph_replay_us(torch, make_call, out, calls=20, replays=20):
+    """Per-call time of `calls` back-to-back calls captured in one HIP graph
+    (torch.cuda.CUDAGraph on ROCm) and replayed `replays` times, as a serving
+    loop runs a captured decode step.  `make_call` must read the current
+    stream when it is called.  Every replay's `out` must equal the eager
+    result."""
+    make_call()()
+    torch.cuda.synchronize()
+    eager = out.clone()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        fn = make_call()
+        for _ in range(calls):
+            fn()
+    times = []
+    for _ in range(replays):
+        out.zero_()
+        torch.cuda.synchronize()
+        start = torch.cuda.Event(enable_timing=True)
+        stop = torch.cuda.Event(enable_timing=True)
+        start.record()
+        graph.replay()
+        stop.record()
+        stop.synchronize()
+        times.append(start.elapsed_time(stop) * 1000.0 / calls)
+        if not torch.equal(out, eager):
+            raise RuntimeError("graph replay differs from the eager call")
+    del graph
     return statistics.median(times)
 
 
@@ -522,6 +554,8 @@ def main():
         "pct_peak": round(100 * gbs / HBM_PEAK_GBS, 1),
         "single_partition_us": round(median_us(torch, c5.call(cx, workspace=False)), 3),
         "reference_protocol_us": round(median_us(torch, call), 3),
+        "graph_replay_us": round(graph_replay_us(torch, lambda: c5.call(cx, workspace=True),
+                                                 c5.out), 3),
     }
     if want("c1"):
         results["c1_decode"] = bench_c1(cx)
