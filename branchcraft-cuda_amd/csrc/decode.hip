@@ -206,7 +206,6 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == kMaxWaves ? 3 : 2) void paged_
   const int g4 = lane >> 4;   // k-slice group / output row group
   const int c16 = lane & 15;  // token row of A, head column of B and C
 
-  // blockIdx.x = range * zgroups + zg; wave -> head block z.
   // Flat mode: blockIdx.x = range * zgroups + zg, wave -> head block z.
   // Sliced mode (nwg == 0): blockIdx.x = sequence * zdim + z, every wave on
   // head block z, wave w on the w-th of WAVES shares of the sequence's pages.

@@ -4,10 +4,12 @@
 // impls under the CUDA dispatch key at :150-154; on PyTorch-ROCm the CUDA
 // key is the HIP device key).  Each impl validates its tensors with
 // TORCH_CHECK (RuntimeError on failure, same rules as the reference), then
-// calls the C ABI in include/branchcraft.h on the current HIP stream.
+// calls the C ABI in include/branchcraft.h on the current HIP stream of the
+// tensors' device, which it makes current for the call.
 // Workspaces for split launches come from PyTorch's caching allocator, which
 // keeps the ops safe under HIP graph capture.
 #include <ATen/ATen.h>
+#include <c10/core/DeviceGuard.h>
 #include <c10/hip/HIPStream.h>
 #include <torch/library.h>
 
@@ -75,6 +77,7 @@ at::Tensor tree_verify_hip(const at::Tensor& q, const at::Tensor& prefix_k,
                   q.device() == pages.device() && q.device() == lengths.device() &&
                   q.device() == parent.device(),
               "all tensors must share a device");
+  const c10::DeviceGuard guard(q.device());
   auto output = at::empty(q.sizes(), q.options().dtype(at::kFloat));
   TORCH_CHECK(pages.size(1) >= 1, "pages must have at least one column");
   bc_shape shape{int(b), int(hq), int(hkv), int(d), int(pages.size(1)),
@@ -139,6 +142,7 @@ at::Tensor packed_decode_out_hip(const at::Tensor& q, const at::Tensor& packed_k
   TORCH_CHECK(q.device() == packed_kv.device() && q.device() == pages.device() &&
                   q.device() == lengths.device() && q.device() == output.device(),
               "all tensors must share a device");
+  const c10::DeviceGuard guard(q.device());
   bc_shape shape{int(b), int(hq), int(hkv), int(d), int(pages.size(1)),
                  int(packed_kv.size(0))};
   const size_t ws_bytes = bc_packed_decode_workspace_size(shape);
@@ -183,6 +187,7 @@ void commit_path_hip(at::Tensor& cache_k, at::Tensor& cache_v,
                   cache_k.device() == dest_pages.device() &&
                   cache_k.device() == dest_slots.device(),
               "all tensors must share a device");
+  const c10::DeviceGuard guard(cache_k.device());
   bc_shape shape{int(b), int(hkv), int(hkv), int(d), 1, int(cache_k.size(0))};
   check_launch(bc_commit_path(shape, hptr(draft_k), hptr(draft_v), hptr_mut(cache_k),
                               hptr_mut(cache_v), path_nodes.data_ptr<int>(),
@@ -225,6 +230,7 @@ void commit_paths_hip(at::Tensor& cache_k, at::Tensor& cache_v,
                   cache_k.device() == dest_pages.device() &&
                   cache_k.device() == dest_slots.device(),
               "all tensors must share a device");
+  const c10::DeviceGuard guard(cache_k.device());
   bc_shape shape{int(b), int(hkv), int(hkv), int(d), 1, int(cache_k.size(0))};
   check_launch(bc_commit_paths(shape, hptr(draft_k), hptr(draft_v), hptr_mut(cache_k),
                                hptr_mut(cache_v), requests.data_ptr<int>(),
@@ -250,6 +256,7 @@ void copy_pages_hip(at::Tensor& cache_k, at::Tensor& cache_v,
                   cache_k.device() == src_pages.device() &&
                   cache_k.device() == dst_pages.device(),
               "all tensors must share a device");
+  const c10::DeviceGuard guard(cache_k.device());
   bc_shape shape{1, int(cache_k.size(2)), int(cache_k.size(2)), int(cache_k.size(3)), 1,
                  int(cache_k.size(0))};
   check_launch(bc_copy_pages(shape, hptr_mut(cache_k), hptr_mut(cache_v),
