@@ -96,49 +96,67 @@ __device__ __forceinline__ int wave_incl_scan_i(int x, int lane) {
   return x;
 }
 
-// Total pages of the batch and the page count per workgroup (flat mode).
-__device__ void flat_geometry(const AttnParams& P, int lane, int& total, int& per) {
-  int t = 0;
-  for (int base = 0; base < P.batch; base += 64)
-    t += wave_sum_i(base + lane < P.batch ? seq_pages(P, base + lane) : 0);
-  total = t;
-  per = (t + P.nwg - 1) / P.nwg;
+__device__ __forceinline__ int pages_of(int len) {
+  return (len + BC_PAGE_SIZE - 1) / BC_PAGE_SIZE;
 }
 
-// The sequence with the rank-th most pages (ties by index).  Workgroups are
-// dispatched in index order, so giving the lowest indices the longest
-// sequences balances the rounds of one-workgroup-per-sequence launches.
-// Single sequences and batches above 64 sequences keep index order.
-__device__ int seq_by_rank(const AttnParams& P, int lane, int rank) {
-  if (P.batch == 1 || P.batch > 64) return rank;
-  const int n = lane < P.batch ? seq_pages(P, lane) : -1;
+// Flat mode: workgroup rid's share of the batch's pages, `count` pages of
+// the concatenated sequences from local page `plocal` of sequence b, whose
+// length is len.  Lane i keeps sequence i's length in a register, so a batch
+// of up to 64 sequences costs one round of loads before the first page id
+// (larger batches load the lengths again for the search).
+__device__ void flat_range(const AttnParams& P, int lane, int rid, int& b, int& plocal,
+                           int& count, int& len) {
+  const int len0 = lane < P.batch ? seq_len(P, lane) : 0;
+  int total = wave_sum_i(pages_of(len0));
+  for (int base = 64; base < P.batch; base += 64)
+    total += wave_sum_i(base + lane < P.batch ? seq_pages(P, base + lane) : 0);
+  const int per = (total + P.nwg - 1) / P.nwg;
+  const int f0 = rid * per;
+  count = min(total, f0 + per) - f0;
+  b = 0;
+  plocal = 0;
+  len = 0;
+  if (count <= 0) return;
+  int run = 0;  // pages before sequence `base`
+  for (int base = 0; base < P.batch; base += 64) {
+    const int l = base == 0 ? len0 : (base + lane < P.batch ? seq_len(P, base + lane) : 0);
+    const int n = pages_of(l);
+    const int inc = wave_incl_scan_i(n, lane);
+    const int tot = __builtin_amdgcn_readlane(inc, 63);
+    if (run + tot > f0) {
+      const unsigned long long hit = __builtin_amdgcn_ballot_w64(run + inc > f0);
+      const int first = __builtin_ffsll((long long)hit) - 1;
+      b = base + first;
+      plocal = f0 - run - __builtin_amdgcn_readlane(inc - n, first);
+      len = __builtin_amdgcn_readlane(l, first);
+      return;
+    }
+    run += tot;
+  }
+}
+
+// The sequence with the rank-th most pages (ties by index) and its length.
+// Workgroups are dispatched in index order, so giving the lowest indices the
+// longest sequences balances the rounds of one-workgroup-per-sequence
+// launches.  Single sequences and batches above 64 sequences keep index
+// order.
+__device__ int seq_by_rank(const AttnParams& P, int lane, int rank, int& len) {
+  if (P.batch == 1 || P.batch > 64) {
+    len = seq_len(P, rank);
+    return rank;
+  }
+  const int l = lane < P.batch ? seq_len(P, lane) : 0;
+  const int n = lane < P.batch ? pages_of(l) : -1;
   int r = 0;
   for (int k = 0; k < P.batch; ++k) {
     const int nk = __builtin_amdgcn_readlane(n, k);
     r += (nk > n || (nk == n && k < lane)) ? 1 : 0;
   }
   const unsigned long long hit = __builtin_amdgcn_ballot_w64(lane < P.batch && r == rank);
-  return __builtin_ffsll((long long)hit) - 1;
-}
-
-// Sequence holding flat page f (f < total) and the flat index of its first page.
-__device__ void locate(const AttnParams& P, int lane, int f, int& b, int& start) {
-  int run = 0;
-  for (int base = 0; base < P.batch; base += 64) {
-    const int n = base + lane < P.batch ? seq_pages(P, base + lane) : 0;
-    const int inc = wave_incl_scan_i(n, lane);
-    const int tot = __builtin_amdgcn_readlane(inc, 63);
-    if (run + tot > f) {
-      const unsigned long long hit = __builtin_amdgcn_ballot_w64(run + inc > f);
-      const int first = __builtin_ffsll((long long)hit) - 1;
-      b = base + first;
-      start = run + __builtin_amdgcn_readlane(inc - n, first);
-      return;
-    }
-    run += tot;
-  }
-  b = P.batch - 1;
-  start = run;
+  const int b = __builtin_ffsll((long long)hit) - 1;
+  len = __builtin_amdgcn_readlane(l, b);
+  return b;
 }
 
 template <typename OutT>
@@ -222,25 +240,17 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == kMaxWaves ? 3 : 2) void paged_
 
   // This workgroup's pages: sequence pb from local page `plocal`, `count`
   // pages in all (crossing into later sequences in flat mode).
-  int pb, plocal, count;
+  int pb, plocal, count, plen;
   if (sliced) {
-    pb = seq_by_rank(P, lane, rid);
-    const int np = seq_pages(P, pb);
+    pb = seq_by_rank(P, lane, rid, plen);
+    const int np = pages_of(plen);
     plocal = wave * np / WAVES;
     count = (wave + 1) * np / WAVES - plocal;  // may be 0 (an empty slice)
   } else {
-    int total, per;
-    flat_geometry(P, lane, total, per);
-    const int f0 = rid * per;
-    const int f1 = min(total, f0 + per);
-    if (f0 >= f1) return;
-    int start;
-    locate(P, lane, f0, pb, start);
-    plocal = f0 - start;
-    count = f1 - f0;
+    flat_range(P, lane, rid, pb, plocal, count, plen);
+    if (count <= 0) return;
   }
-  int ppages = seq_pages(P, pb);
-  int plen = seq_len(P, pb);
+  int ppages = pages_of(plen);
   int seg0 = plocal;  // first local page of pb in this range
 
   // Q^T B operand: lane holds Q[head h0+c16][32s + 8*g4 .. +8].
@@ -491,7 +501,7 @@ __global__ __launch_bounds__(256) void merge_kernel(AttnParams P) {
   const int rowi = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (rowi >= P.batch * P.hq) return;
   const int b = rowi / P.hq, h = rowi % P.hq;
-  // One round of length loads: the batch's page total (as flat_geometry),
+  // One round of length loads: the batch's page total (as flat_range),
   // the pages before sequence b and b's own page count.
   int total = 0, before = 0, np = 0;
   for (int base = 0; base < P.batch; base += 64) {
