@@ -104,12 +104,14 @@ def test_head_layouts_beyond_reference(hq, hkv, d, oracle):
         G.gate(out, expected, 3e-4, f"Hq={hq} Hkv={hkv} D={d} splits={splits}")
 
 
-@pytest.mark.parametrize("batch", [40, 64, 70])
+@pytest.mark.parametrize("batch", [40, 64, 70, 130])
 def test_unsplit_ragged_batches(batch, oracle):
     """splits = 1 runs one workgroup per (sequence, head block), and
     workgroup r takes the sequence with the r-th most pages (ties by index)
     for batches of up to 64; larger batches keep index order.  Ragged
-    lengths with ties and empty sequences cover both orders."""
+    lengths with ties and empty sequences cover both orders; with splits,
+    130 sequences make the workgroups' range search cross three blocks of
+    64 lengths."""
     rng = np.random.default_rng(batch)
     lens = rng.integers(0, 300, size=batch)
     lens[::7] = 129

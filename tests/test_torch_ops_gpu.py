@@ -17,6 +17,7 @@ import numpy as np
 import pytest
 import torch
 
+import branchcraft_capi as capi
 import branchcraft_torch as bc
 from oracle import oracle_c
 import gpu_helpers as G
@@ -97,6 +98,37 @@ def test_packed_decode_layouts_and_graph_replay(layout):
         torch.cuda.synchronize()
         assert np.all(np.abs(out.cpu().numpy().astype(np.float32) - exp32) <= tol), f"replay {i}"
         del junk
+
+
+def test_packed_decode_concurrent_streams():
+    """Calls on two streams at once, each with its own workspace from the
+    caching allocator, give the same bits as the same calls one at a time.
+    An 80-column page table takes the split path (workspace and merge)."""
+    torch.manual_seed(23)
+    batch, hq, hkv, dim, pool = 8, 8, 2, 64, 700
+    cache = torch.randn(pool, 2, 16, hkv, dim, device="cuda", dtype=torch.float16)
+    gen = np.random.default_rng(23)
+    pages = torch.from_numpy(
+        np.stack([gen.permutation(pool)[:80] for _ in range(batch)]).astype(np.int32)).cuda()
+    lengths = torch.from_numpy(gen.integers(1000, 1281, size=batch).astype(np.int32)).cuda()
+    qs = [torch.randn(batch, hq, dim, device="cuda", dtype=torch.float16) for _ in range(2)]
+    scale = 1 / math.sqrt(dim)
+    assert G.lib().bc_packed_decode_workspace_size(
+        capi.Shape(batch, hq, hkv, dim, 80, pool)) > 0
+    solo = [bc.packed_decode_out(q, cache, pages, lengths, torch.empty_like(q), scale)
+            for q in qs]
+    torch.cuda.synchronize()
+    outs = [torch.full_like(q, float("nan")) for q in qs]
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    for st in streams:
+        st.wait_stream(torch.cuda.current_stream())
+    for _ in range(5):
+        for st, q, out in zip(streams, qs, outs):
+            with torch.cuda.stream(st):
+                bc.packed_decode_out(q, cache, pages, lengths, out, scale)
+    torch.cuda.synchronize()
+    for i in range(2):
+        assert torch.equal(outs[i], solo[i]), f"stream {i}"
 
 
 def test_packed_decode_opcheck():
