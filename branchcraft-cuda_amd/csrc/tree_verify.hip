@@ -146,19 +146,23 @@ __global__ __launch_bounds__(kThreads, 2) void tree_kernel(TreeParams P) {
   __shared__ int s_parent[BC_MAX_TREE_NODES];
   __shared__ __attribute__((aligned(16))) char s_mem[kWaves * kTile * VP * 2];
   __shared__ float s_m[2][32], s_l[2][32];
-  if (wave == 0) {
-    // Rows past the tile's query rows read row (node 0, head h) and store
-    // zeros; every load is issued before the first store.
+  // The loads before the first barrier go out together and on one path, so
+  // the waits before the LDS stores cover Q and the parents only: the parent
+  // array (one entry per thread, the index clamped so every lane loads),
+  // each wave's quarter of the Q^T fragments and, further down, the first
+  // tile's K.  Rows past the tile's query rows read row (node 0, head h) and
+  // store zeros.
+  static_assert(BC_MAX_TREE_NODES <= kThreads, "one parent entry per thread");
+  constexpr int QS = KS / kWaves;  // Q^T k-steps staged per wave
+  static_assert(QS * kWaves == KS, "Q^T k-steps split evenly over the waves");
+  const bool has_parent = (int)threadIdx.x < P.nodes;
+  const int par = P.parent[(size_t)b * P.nodes + min((int)threadIdx.x, P.nodes - 1)];
+  uint4 qf[QS];
+  {
     const uint16_t* qp = P.dq + (((size_t)b * P.nodes + node) * P.hq + h) * D + 8 * g;
-    uint4 qf[KS];
 #pragma unroll
-    for (int s = 0; s < KS; ++s) qf[s] = ldg16(qp + 16 * s);
-#pragma unroll
-    for (int s = 0; s < KS; ++s) s_q[s][lane] = rvalid ? qf[s] : make_uint4(0, 0, 0, 0);
+    for (int j = 0; j < QS; ++j) qf[j] = ldg16(qp + 16 * (wave * QS + j));
   }
-  if (drafts)
-    for (int i = threadIdx.x; i < P.nodes; i += kThreads)
-      s_parent[i] = P.parent[(size_t)b * P.nodes + i];
 
   _Float16* vs = reinterpret_cast<_Float16*>(s_mem) + wave * kTile * VP;
   // Transpose-read address of this lane: group G = lane/16, j = lane%16.
@@ -347,12 +351,16 @@ __global__ __launch_bounds__(kThreads, 2) void tree_kernel(TreeParams P) {
   bool ta = false, tb = false;
   bool pa[2] = {true, true}, pbk[2] = {true, true};
   int idb[2];
-  // The first tile's loads go out before the barrier that publishes Q and
-  // the parent array.
-  if (nmine > 0) {
-    issue(0, ida, ka, va, ta, pa);
-    ids_of(1, idb);
-  }
+  // The first tile's loads go out before Q and the parent array are stored
+  // and published by the barrier.  A wave without tiles issues them too
+  // (tile_of clamps, and every address stays inside its tensor) so that all
+  // waves run the same code up to the barrier.
+  issue(0, ida, ka, va, ta, pa);
+#pragma unroll
+  for (int j = 0; j < QS; ++j)
+    s_q[wave * QS + j][lane] = rvalid ? qf[j] : make_uint4(0, 0, 0, 0);
+  if (has_parent) s_parent[threadIdx.x] = par;
+  ids_of(1, idb);
   __syncthreads();
   if (nmine > 0) {
     for (int idx = 0; idx < nmine; idx += 2) {
