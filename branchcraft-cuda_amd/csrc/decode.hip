@@ -750,7 +750,7 @@ static int packed_common(bc_shape s, const bc_half* q, const bc_half* kv,
   P.scale_log2 = (float)((double)scale * 1.4426950408889634);
   const int nwg = packed_nwg(s);
   const size_t need = packed_workspace(s, nwg);
-  if (ws && ws_bytes >= need && packed_split(s)) {
+  if (ws && ws_bytes >= need && aligned16(ws) && packed_split(s)) {
     P.nwg = nwg;
     const size_t slots = (size_t)nwg + s.batch;
     const size_t acc_bytes =

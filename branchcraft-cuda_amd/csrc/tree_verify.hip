@@ -615,8 +615,6 @@ extern "C" int bc_tree_verify(bc_shape s, bc_tree_inputs in, int nodes,
 }
 
 extern "C" size_t bc_tree_verify_workspace_size(bc_shape s, int nodes) {
-  bc_tree_inputs dummy{};
-  (void)dummy;
   if (s.batch < 1 || s.query_heads < 1 || s.kv_heads < 1 ||
       s.query_heads % s.kv_heads || (s.dim != 64 && s.dim != 128) ||
       s.max_pages < 1 || nodes < 1 || nodes > BC_MAX_TREE_NODES)
@@ -632,7 +630,7 @@ extern "C" int bc_tree_verify_ws(bc_shape s, bc_tree_inputs in, int nodes,
     return BC_ERROR_INVALID_VALUE;
   int chunk = 0, parts = 0;
   const size_t need = tree_workspace(s, nodes, &chunk, &parts);
-  if (!workspace || need == 0 || workspace_bytes < need)
+  if (!workspace || need == 0 || workspace_bytes < need || !aligned16(workspace))
     return bc_tree_verify(s, in, nodes, stream);
   TreeParams P = make_params(s, in, nodes);
   P.chunk_tokens = chunk;

@@ -83,8 +83,12 @@ typedef struct bc_tree_inputs {
   float* output;
 } bc_tree_inputs;
 
-/* Paged GQA decode with `splits` equal partitions per sequence and an FP32
- * merge of the partial softmax states.
+/* Paged GQA decode.  splits == 1 runs one workgroup per (sequence, head
+ * block), its waves splitting the pages and merging in LDS, with no scratch.
+ * splits > 1 spreads the batch's pages over equal ranges of the concatenated
+ * sequences, at most (splits - 1) * B + 1 workgroups, and merges the FP32
+ * partial softmax states of the sequences a range boundary cuts; the
+ * partials fit the reference's scratch sizes.
  * Replaces branchcraft::decode, include/branchcraft.hpp:39-40
  * (src/paged_gqa.cu:198-208).  Rejects: batch/Hq/Hkv < 1, Hq % Hkv != 0,
  * dim not 64/128, max_pages or physical_pages < 1, splits outside
@@ -110,9 +114,9 @@ size_t bc_tree_verify_workspace_size(bc_shape shape, int nodes);
 
 /* bc_tree_verify with the prefix split into chunks across workgroups and an
  * FP32 merge; `workspace` holds at least bc_tree_verify_workspace_size
- * bytes (256-byte aligned).  A null workspace or workspace_bytes smaller
- * than required falls back to bc_tree_verify.  Results match
- * bc_tree_verify within floating-point reassociation. */
+ * bytes.  A null workspace, one smaller than required or one not aligned to
+ * 16 bytes falls back to bc_tree_verify.  Results match bc_tree_verify
+ * within floating-point reassociation. */
 int bc_tree_verify_ws(bc_shape shape, bc_tree_inputs in, int nodes,
                       void* workspace, size_t workspace_bytes,
                       bc_stream_t stream);
@@ -174,10 +178,13 @@ int bc_packed_decode(bc_shape shape, const bc_half* q, const bc_half* packed_kv,
  * whatever workspace is passed (the bc_auto_splits rule, from the shape only). */
 size_t bc_packed_decode_workspace_size(bc_shape shape);
 
-/* bc_packed_decode with long sequences split into fixed token chunks across
- * workgroups and an FP32 merge; chunking depends on shape.max_pages only,
- * so no device lengths are read on the host.  A null or undersized
- * workspace, or a shape whose workspace size is 0, runs bc_packed_decode. */
+/* bc_packed_decode with the batch's pages spread over equal ranges of the
+ * concatenated sequences, two workgroups per CU, and an FP32 merge of the
+ * sequences a range boundary cuts.  The workgroup count and the workspace
+ * size depend on the shape and the device's CU count only; the kernels find
+ * the ranges from the lengths on the device, so no lengths are read on the
+ * host.  A null workspace, one smaller than required or not aligned to 16
+ * bytes, or a shape whose workspace size is 0, runs bc_packed_decode. */
 int bc_packed_decode_ws(bc_shape shape, const bc_half* q,
                         const bc_half* packed_kv, const int32_t* pages,
                         const int32_t* lengths, bc_half* output,

@@ -50,7 +50,9 @@ def decode(q, k, v, pages, lengths, splits, *, keep=False, out=None):
     return o.cpu().numpy()
 
 
-def tree(k, v, pages, lengths, dq, dk, dv, parent, *, workspace=True):
+def tree(k, v, pages, lengths, dq, dk, dv, parent, *, workspace=True, ws_offset=0):
+    """ws_offset shifts the workspace pointer by that many bytes (the size
+    passed stays the required one)."""
     b, n, hq, d = dq.shape
     P, _, hkv, _ = k.shape
     tk, tv = dev(k), dev(v)
@@ -66,8 +68,8 @@ def tree(k, v, pages, lengths, dq, dk, dv, parent, *, workspace=True):
     L = lib()
     if workspace:
         nbytes = L.bc_tree_verify_workspace_size(shape, n)
-        ws = torch.empty(max(1, nbytes), device="cuda", dtype=torch.uint8)
-        check(L.bc_tree_verify_ws(shape, ins, n, ws.data_ptr(), nbytes, stream()),
+        ws = torch.empty(max(1, nbytes + ws_offset), device="cuda", dtype=torch.uint8)
+        check(L.bc_tree_verify_ws(shape, ins, n, ws.data_ptr() + ws_offset, nbytes, stream()),
               "bc_tree_verify_ws")
     else:
         check(L.bc_tree_verify(shape, ins, n, stream()), "bc_tree_verify")
@@ -76,9 +78,10 @@ def tree(k, v, pages, lengths, dq, dk, dv, parent, *, workspace=True):
 
 
 def packed(q, cache: torch.Tensor, strides, hkv, phys_pages, pages, lengths, scale, *,
-           workspace=True):
+           workspace=True, ws_offset=0):
     """cache: a GPU FP16 tensor whose storage holds the packed pool; strides
-    are element strides relative to cache.data_ptr()."""
+    are element strides relative to cache.data_ptr().  ws_offset shifts the
+    workspace pointer by that many bytes."""
     b, hq, d = q.shape
     tq = dev(q)
     tp, tl = dev(pages.astype(np.int32)), dev(lengths.astype(np.int32))
@@ -88,10 +91,11 @@ def packed(q, cache: torch.Tensor, strides, hkv, phys_pages, pages, lengths, sca
     L = lib()
     if workspace:
         nbytes = L.bc_packed_decode_workspace_size(shape)
-        ws = torch.empty(max(1, nbytes), device="cuda", dtype=torch.uint8)
+        ws = torch.empty(max(1, nbytes + ws_offset), device="cuda", dtype=torch.uint8)
         check(L.bc_packed_decode_ws(shape, tq.data_ptr(), cache.data_ptr(), tp.data_ptr(),
                                     tl.data_ptr(), o.data_ptr(), bs, hs, ss, kvs,
-                                    float(scale), ws.data_ptr(), nbytes, stream()),
+                                    float(scale), ws.data_ptr() + ws_offset, nbytes,
+                                    stream()),
               "bc_packed_decode_ws")
     else:
         check(L.bc_packed_decode(shape, tq.data_ptr(), cache.data_ptr(), tp.data_ptr(),

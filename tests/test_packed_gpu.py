@@ -124,3 +124,21 @@ def test_config5_full_size(oracle):
         out = G.packed(q, cache, strides, hkv, NB, pages, lengths, scale, workspace=ws)
         err = np.abs(out.astype(np.float32) - exp32)
         assert np.all(err <= G.f16_tolerance(exp32, 2e-3)), f"ws={ws} max err {err.max():.3e}"
+
+
+def test_misaligned_workspace_runs_unsplit():
+    """A workspace that is not 16-byte aligned is ignored: the call gives the
+    same bits as the call without one."""
+    torch.manual_seed(41)
+    rng = np.random.default_rng(41)
+    B, hq, hkv, d, NB = 4, 8, 2, 64, 300
+    cache = torch.randn((NB, 2, 16, hkv, d), device="cuda", dtype=torch.float16)
+    lengths = rng.integers(900, 1281, size=B).astype(np.int32)
+    pages = np.stack([rng.permutation(NB)[:80] for _ in range(B)]).astype(np.int32)
+    q = rng.standard_normal((B, hq, d)).astype(np.float16)
+    strides = (cache.stride(0), cache.stride(3), cache.stride(2), cache.stride(1))
+    assert G.lib().bc_packed_decode_workspace_size(capi.Shape(B, hq, hkv, d, 80, NB)) > 0
+    plain = G.packed(q, cache, strides, hkv, NB, pages, lengths, 0.125, workspace=False)
+    shifted = G.packed(q, cache, strides, hkv, NB, pages, lengths, 0.125, workspace=True,
+                       ws_offset=4)
+    assert np.array_equal(plain, shifted)

@@ -12,6 +12,7 @@ import numpy as np
 import pytest
 
 from oracle import oracle_np
+import branchcraft_capi as capi
 import gpu_helpers as G
 
 pytestmark = pytest.mark.gpu
@@ -101,3 +102,17 @@ def test_garbage_past_prefix_is_ignored(oracle):
     for ws in (False, True):
         G.gate(G.tree(k, v, pages, lengths, dq, dk, dv, par, workspace=ws), expected, 3e-4,
                "garbage slots")
+
+
+def test_misaligned_workspace_runs_single_pass():
+    """A workspace that is not 16-byte aligned is ignored: the call gives the
+    same bits as bc_tree_verify."""
+    rng = np.random.default_rng(43)
+    fix = oracle_np.tree_fixture(rng, 2, 600, 7, parents="random")
+    k, v, pages, lengths, dq, dk, dv, par = fix
+    b, n, hq, d = dq.shape
+    shape = capi.Shape(b, hq, k.shape[2], d, pages.shape[1], k.shape[0])
+    assert G.lib().bc_tree_verify_workspace_size(shape, n) > 0
+    plain = G.tree(*fix, workspace=False)
+    shifted = G.tree(*fix, workspace=True, ws_offset=4)
+    assert np.array_equal(plain, shifted)
