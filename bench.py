@@ -14,7 +14,8 @@ warm-ups, 7 trials x 20 launches, median; src/main.cu:354-373):
   C3 tree_verify 8 x (2048+5) shared prefix vs the expanded-prefix decode,
      plus the copy-on-write commit;  C4 split-K decode B=4, L~U[16K, 32K];
   C5 packed decode without the workspace (single partition per sequence),
-     and 20 calls captured in one HIP graph and replayed (per-call time).
+     and 20 calls captured in one HIP graph and replayed (per-call time);
+     paged decode (bc_decode, separate K and V) on the same C5 sequences.
 The CPU baseline times the C oracle (oracle/bc_oracle.c) on the whole C5
 workload on this host's cores.
 
@@ -272,6 +273,39 @@ class C5:
         return f
 
 
+def bench_c5_paged(cx, c5):
+    """bc_decode (separate [P, 16, Hkv, D] K and V, FP32 output) on the config-5
+    sequences: the same lengths, page table, Q and K/V values as the packed
+    call, so its output must match the packed output up to FP16 rounding."""
+    t = cx.torch
+    k = c5.cache[:, 0].contiguous()
+    v = c5.cache[:, 1].contiguous()
+    out = t.empty((c5.B, c5.hq, c5.d), device="cuda", dtype=t.float32)
+    shape = cx.capi.Shape(c5.B, c5.hq, c5.hkv, c5.d, c5.maxp, c5.nb)
+    auto = cx.lib.bc_auto_splits(shape, int(c5.lengths.max()), cx.cus)
+    nbytes = decode_bytes(c5.lengths, c5.hq, c5.hkv, c5.d, 4)
+    res = {"auto_splits": auto}
+    for splits in sorted({1, auto}):
+        scr = decode_scratch(cx, c5.B, c5.hq, c5.d, splits)
+        call = make_decode_call(cx, c5.q, k, v, c5.tp, c5.tl, out, splits, scr)
+        us = median_us(t, call)
+        res[f"splits{splits}_us"] = round(us, 3)
+    call()
+    c5.call(cx, workspace=True)()
+    t.cuda.synchronize()
+    diff = float((out - c5.out.float()).abs().max())
+    if diff > 2e-3:
+        raise RuntimeError(f"paged and packed decode differ by {diff}")
+    us = res[f"splits{auto}_us"]
+    res.update(bytes=nbytes, us=us, gbs=round(nbytes / us / 1e3, 1),
+               pct_peak=round(100 * nbytes / us / 1e3 / HBM_PEAK_GBS, 1),
+               max_abs_diff_vs_packed=diff,
+               workload="paged decode (bc_decode, auto splits) on the config-5 sequences, "
+                        "FP32 output")
+    del k, v
+    return res
+
+
 def tree_setup(cx, batch, prefix, seed):
     """Shared-prefix tree fixture on the GPU: every request's page-table row
     names the same physical pages (random permutation of the pool)."""
@@ -400,7 +434,10 @@ def bench_tree(cx, batch, prefix, seed, with_expanded):
         exp_bytes = decode_bytes(lens, f["hq"], f["hkv"], f["d"], 4)
         shape = cx.capi.Shape(q.shape[0], f["hq"], f["hkv"], f["d"], ep.shape[1], ek.shape[0])
         auto = cx.lib.bc_auto_splits(shape, max(lens), cx.cus)
-        for splits in sorted({1, auto}):
+        # The baseline is the best of the heuristic's split count, its
+        # neighbours and the unsplit kernel, so the tree is not compared with
+        # an unlucky split.
+        for splits in sorted({1, max(1, auto - 1), auto, auto + 1}):
             scr = decode_scratch(cx, q.shape[0], f["hq"], f["d"], splits)
             fn = make_decode_call(cx, q, ek, ev, ep, el, out, splits, scr)
             us = median_us(t, fn)
@@ -557,6 +594,8 @@ def main():
         "graph_replay_us": round(graph_replay_us(torch, lambda: c5.call(cx, workspace=True),
                                                  c5.out), 3),
     }
+    results["c5_paged_decode"] = bench_c5_paged(cx, c5)
+    print(f"[bench] C5 paged {results['c5_paged_decode']}", file=sys.stderr, flush=True)
     if want("c1"):
         results["c1_decode"] = bench_c1(cx)
         print(f"[bench] C1 {results['c1_decode']}", file=sys.stderr, flush=True)

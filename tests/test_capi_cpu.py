@@ -149,10 +149,11 @@ def test_packed_rejects(strides, scale):
 
 
 def test_auto_splits_policy():
-    """Split decode runs (splits - 1) * batch + 1 flat page ranges, each
-    served by ceil(kv head blocks / 4) four-wave workgroups; the heuristic
-    picks the most ranges whose workgroups fit one per CU, and keeps short
-    contexts unsplit."""
+    """Split decode runs (splits - 1) * batch + 1 flat page ranges, rounded
+    down to whole waves of one workgroup per CU, each range served by
+    ceil(kv head blocks / 4) four-wave workgroups; the heuristic picks the
+    fewest splits that fill a wave, and keeps short contexts and batches of a
+    wave or more unsplit."""
     lib = capi.load()
     assert lib.bc_auto_splits(_shape(batch=1), 63, 256) == 1  # tiny contexts stay whole
     # short contexts whose (sequence, head block) workgroups fit the CUs run
@@ -162,14 +163,16 @@ def test_auto_splits_policy():
     assert lib.bc_auto_splits(_shape(batch=33), 1024, 256) > 1
     assert lib.bc_auto_splits(_shape(batch=1), 1025, 256) > 1
     ranges = 256 // 2  # 8 KV heads: two four-wave workgroups per range
-    for batch in (1, 4, 16, 64, 200):
+    for batch in (1, 2, 4, 16, 64, 100, 127):
         s = lib.bc_auto_splits(_shape(batch=batch), 32768, 256)
         assert 1 <= s <= capi.BC_MAX_SPLITS
-        assert (s - 1) * batch + 1 <= ranges
-        if s < capi.BC_MAX_SPLITS:
-            assert s * batch + 1 > ranges  # one more split would overflow the CUs
-    assert lib.bc_auto_splits(_shape(batch=4), 32768, 256) == 32
-    assert lib.bc_auto_splits(_shape(batch=512), 4096, 256) == 1
+        assert (s - 1) * batch + 1 >= ranges  # a full wave of workgroups
+        assert (s - 2) * batch + 1 < ranges  # one split fewer would leave CUs idle
+    assert lib.bc_auto_splits(_shape(batch=1), 32768, 256) == 128
+    assert lib.bc_auto_splits(_shape(batch=4), 32768, 256) == 33
+    assert lib.bc_auto_splits(_shape(batch=64), 4096, 256) == 3
+    for batch in (128, 200, 512):
+        assert lib.bc_auto_splits(_shape(batch=batch), 4096, 256) == 1
     # sixteen KV heads: four workgroups per range
     assert lib.bc_auto_splits(_shape(batch=1, query_heads=16, kv_heads=16), 4096, 256) == 64
 
