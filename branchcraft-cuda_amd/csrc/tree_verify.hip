@@ -564,7 +564,14 @@ void tree_chunking(const bc_shape& s, int nodes, int* chunk_tokens, int* parts) 
   const long long units =
       (long long)s.batch * s.kv_heads * ((nodes * group + 31) / 32);
   const int max_tokens = s.max_pages * BC_PAGE_SIZE;
-  long long want = bch::device_cus() / units - 1;
+  const int cus = bch::device_cus();
+  long long want = cus / units - 1;
+  // With units in (cus/3, cus/2] the rule above gives a single chunk, which
+  // leaves half or more of the CUs idle while each workgroup walks the whole
+  // prefix; two chunks plus the draft part keep every workgroup resident (two
+  // per CU) and measured 25-26 us against 35 us at 12 and 16 requests of a
+  // 2048-token prefix.  More units than that measured slower with two.
+  if (want < 2 && 2LL * units <= cus) want = 2;
   if (want < 1) want = 1;
   int chunk = (int)((max_tokens + want - 1) / want);
   chunk = (chunk + kTile - 1) / kTile * kTile;

@@ -191,6 +191,12 @@ def test_workspace_sizes():
     c3 = capi.Shape(8, 32, 8, 128, 129, 160)
     assert lib.bc_tree_verify_workspace_size(c3, 7) > 0
     assert lib.bc_tree_verify_workspace_size(c3, 0) == 0
+    # Trees split the prefix while (request, KV head, row tile) units number at
+    # most half the CUs (two chunks plus the draft part per unit), and run in
+    # one pass beyond that.
+    for batch, split in ((12, True), (16, True), (17, False), (20, False), (32, False)):
+        size = lib.bc_tree_verify_workspace_size(capi.Shape(batch, 32, 8, 128, 129, 160), 7)
+        assert (size > 0) == split, batch
 
 
 def test_torch_ops_register_reference_schemas():

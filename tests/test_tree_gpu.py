@@ -104,6 +104,19 @@ def test_garbage_past_prefix_is_ignored(oracle):
                "garbage slots")
 
 
+def test_mid_batch_splits_the_prefix(oracle):
+    """Sixteen requests: 128 (request, KV head, row tile) units, half the
+    CUs, so the workspace call splits each prefix in two chunks plus the
+    draft part."""
+    rng = np.random.default_rng(16)
+    fix = oracle_np.tree_fixture(rng, 16, 700, 7, parents="random")
+    k, v, pages, lengths, dq, dk, dv, par = fix
+    b, n, hq, d = dq.shape
+    shape = capi.Shape(b, hq, k.shape[2], d, pages.shape[1], k.shape[0])
+    assert G.lib().bc_tree_verify_workspace_size(shape, n) > 0
+    _check(fix, oracle, atol=3e-4, what="B=16")
+
+
 def test_misaligned_workspace_runs_single_pass():
     """A workspace that is not 16-byte aligned is ignored: the call gives the
     same bits as bc_tree_verify."""
