@@ -490,15 +490,23 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == kMaxWaves ? 3 : 2) void paged_
 
 // Flat mode: out = sum_w 2^(m_w - M) a_w / sum_w 2^(m_w - M) l_w over the
 // workgroups whose ranges cut sequence b (src/paged_gqa.cu:76-106); empty
-// sequences give zeros.  One wave per (b, h) output row, two dependent
-// memory rounds: the lengths (page geometry), then every partial's (max,
-// sum) together with the first eight partials' accumulators; lane i holds
-// partial i's weight and every lane accumulates its dims.
-template <int D, typename OutT>
+// sequences give zeros.  RW waves per (b, h) output row (1 or 4), two
+// dependent memory rounds: the lengths (page geometry), then every partial's
+// (max, sum) together with the first eight partials' accumulators; lane i
+// holds partial i's weight and every lane accumulates its dims.  With RW = 4
+// each wave combines a contiguous quarter of the row's partials and wave 0
+// merges the four states through LDS: rows of a few long sequences have
+// hundreds of partials, too many for one wave.
+template <int D, typename OutT, int RW>
 __global__ __launch_bounds__(256) void merge_kernel(AttnParams P) {
+  static_assert(RW == 1 || RW == 4, "one or four waves per row");
   constexpr int PER = D / 64;
   const int lane = threadIdx.x & 63;
-  const int rowi = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int wave = threadIdx.x >> 6;
+  const int sub = wave % RW;  // this wave's share of the row's partials
+  const int rowi = blockIdx.x * (4 / RW) + wave / RW;
+  // Every exit before the LDS merge below is uniform over a row, so with
+  // RW = 4 the whole workgroup leaves together.
   if (rowi >= P.batch * P.hq) return;
   const int b = rowi / P.hq, h = rowi % P.hq;
   // One round of length loads: the batch's page total (as flat_range),
@@ -512,13 +520,18 @@ __global__ __launch_bounds__(256) void merge_kernel(AttnParams P) {
     if (b >= base && b < base + 64) np = __builtin_amdgcn_readlane(n, b - base);
   }
   if (np == 0) {
+    if (sub == 0) {
 #pragma unroll
-    for (int j = 0; j < PER; ++j) store_out<OutT>(P.out, (size_t)rowi * D + lane + 64 * j, 0.f);
+      for (int j = 0; j < PER; ++j) store_out<OutT>(P.out, (size_t)rowi * D + lane + 64 * j, 0.f);
+    }
     return;
   }
   const int per = (total + P.nwg - 1) / P.nwg;
   const int w0 = before / per, w1 = (before + np - 1) / per;
   if (w0 == w1) return;  // the sequence ended inside one range: written directly
+  // This wave's partials: [r0, r1] (empty when r1 < r0).
+  const int nparts = w1 - w0 + 1;
+  const int r0 = w0 + sub * nparts / RW, r1 = w0 + (sub + 1) * nparts / RW - 1;
   float mm = kNegInf, lsum = 0.f, a[PER];
 #pragma unroll
   for (int j = 0; j < PER; ++j) a[j] = 0.f;
@@ -533,8 +546,8 @@ __global__ __launch_bounds__(256) void merge_kernel(AttnParams P) {
       for (int j = 0; j < PER; ++j) v[u][j] = src[64 * j];
     }
   };
-  for (int wb = w0; wb <= w1; wb += 64) {
-    const int cnt = min(64, w1 - wb + 1);
+  for (int wb = r0; wb <= r1; wb += 64) {
+    const int cnt = min(64, r1 - wb + 1);
     // The (max, sum) loads and the first step's partials go out together:
     // the partial loads do not depend on the weights.
     const size_t r = (size_t)(wb + min(lane, cnt - 1) + b) * P.hq + h;
@@ -566,6 +579,32 @@ __global__ __launch_bounds__(256) void merge_kernel(AttnParams P) {
 #pragma unroll
         for (int j = 0; j < PER; ++j) a[j] += wi * v[u][j];
       }
+    }
+  }
+  if constexpr (RW > 1) {
+    __shared__ float xa[RW][D];
+    __shared__ float xml[RW][2];
+#pragma unroll
+    for (int j = 0; j < PER; ++j) xa[sub][lane + 64 * j] = a[j];
+    if (lane == 0) {
+      xml[sub][0] = mm;
+      xml[sub][1] = lsum;
+    }
+    __syncthreads();
+    if (sub != 0) return;
+    float mx = kNegInf;
+#pragma unroll
+    for (int q = 0; q < RW; ++q) mx = __builtin_fmaxf(mx, xml[q][0]);
+    const float ms = safe_max(mx);
+    lsum = 0.f;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) a[j] = 0.f;
+#pragma unroll
+    for (int q = 0; q < RW; ++q) {
+      const float wq = fast_exp2(xml[q][0] - ms);  // 0 for a wave without partials
+      lsum += wq * xml[q][1];
+#pragma unroll
+      for (int j = 0; j < PER; ++j) a[j] += wq * xa[q][lane + 64 * j];
     }
   }
   const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
@@ -601,7 +640,11 @@ hipError_t launch_dim(const AttnParams& P, bool vec, hipStream_t st) {
   hipError_t err = hipGetLastError();
   if (err != hipSuccess || P.nwg == 0) return err;
   const unsigned rows = (unsigned)P.batch * P.hq;
-  merge_kernel<D, OutT><<<dim3((rows + 3) / 4), 256, 0, st>>>(P);
+  // Four waves per row once the ranges outnumber the sequences 16 to 1.
+  if (P.nwg >= 16 * P.batch)
+    merge_kernel<D, OutT, 4><<<dim3(rows), 256, 0, st>>>(P);
+  else
+    merge_kernel<D, OutT, 1><<<dim3((rows + 3) / 4), 256, 0, st>>>(P);
   return hipGetLastError();
 }
 

@@ -126,6 +126,36 @@ def test_config5_full_size(oracle):
         assert np.all(err <= G.f16_tolerance(exp32, 2e-3)), f"ws={ws} max err {err.max():.3e}"
 
 
+@pytest.mark.parametrize("lens", [[32768], [30000, 700]], ids=["one-32k", "long-and-short"])
+def test_long_sequences_many_partials(lens, oracle):
+    """A few long sequences cut by most of the 256 flat ranges: each output row
+    has up to 256 partials, combined by four waves (a quarter each) and then
+    through LDS."""
+    torch.manual_seed(len(lens))
+    rng = np.random.default_rng(len(lens))
+    B, hq, hkv, d = len(lens), 32, 8, 128
+    maxp = -(-max(lens) // 16)
+    NB = sum(-(-n // 16) for n in lens) + 8
+    cache = torch.randn((NB, 2, 16, hkv, d), device="cuda", dtype=torch.float16)
+    lengths = np.array(lens, dtype=np.int32)
+    perm = rng.permutation(NB).astype(np.int32)
+    pages = np.full((B, maxp), -1, dtype=np.int32)
+    cur = 0
+    for i, n in enumerate(lens):
+        c = -(-n // 16)
+        pages[i, :c] = perm[cur:cur + c]
+        cur += c
+    q = rng.standard_normal((B, hq, d)).astype(np.float16)
+    strides = (cache.stride(0), cache.stride(3), cache.stride(2), cache.stride(1))
+    scale = 1 / math.sqrt(d)
+    assert G.lib().bc_packed_decode_workspace_size(capi.Shape(B, hq, hkv, d, maxp, NB)) > 0
+    exp32, _ = oracle.packed_decode(q, cache.cpu().numpy(), pages, lengths, strides, hkv,
+                                    scale, threads=16)
+    out = G.packed(q, cache, strides, hkv, NB, pages, lengths, scale, workspace=True)
+    err = np.abs(out.astype(np.float32) - exp32)
+    assert np.all(err <= G.f16_tolerance(exp32, 2e-3)), f"max err {err.max():.3e}"
+
+
 def test_misaligned_workspace_runs_unsplit():
     """A workspace that is not 16-byte aligned is ignored: the call gives the
     same bits as the call without one."""
