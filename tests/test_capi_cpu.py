@@ -152,8 +152,8 @@ def test_auto_splits_policy():
     """Split decode runs (splits - 1) * batch + 1 flat page ranges, rounded
     down to whole waves of one workgroup per CU, each range served by
     ceil(kv head blocks / 4) four-wave workgroups; the heuristic picks the
-    fewest splits that fill a wave, and keeps short contexts and batches of a
-    wave or more unsplit."""
+    fewest splits that fill a wave, two splits for batches of one to two waves,
+    and keeps short contexts and larger batches unsplit."""
     lib = capi.load()
     assert lib.bc_auto_splits(_shape(batch=1), 63, 256) == 1  # tiny contexts stay whole
     # short contexts whose (sequence, head block) workgroups fit the CUs run
@@ -171,8 +171,8 @@ def test_auto_splits_policy():
     assert lib.bc_auto_splits(_shape(batch=1), 32768, 256) == 128
     assert lib.bc_auto_splits(_shape(batch=4), 32768, 256) == 33
     assert lib.bc_auto_splits(_shape(batch=64), 4096, 256) == 3
-    for batch in (128, 200, 512):
-        assert lib.bc_auto_splits(_shape(batch=batch), 4096, 256) == 1
+    for batch, splits in ((128, 2), (200, 2), (256, 2), (257, 1), (512, 1)):
+        assert lib.bc_auto_splits(_shape(batch=batch), 4096, 256) == splits, batch
     # sixteen KV heads: four workgroups per range
     assert lib.bc_auto_splits(_shape(batch=1, query_heads=16, kv_heads=16), 4096, 256) == 64
 

@@ -156,6 +156,37 @@ def test_long_sequences_many_partials(lens, oracle):
     assert np.all(err <= G.f16_tolerance(exp32, 2e-3)), f"max err {err.max():.3e}"
 
 
+def test_large_batch_takes_split_path(oracle):
+    """128 sequences (one wave of flat ranges at 8 KV heads) run split with a
+    workspace; ragged lengths include empty sequences."""
+    torch.manual_seed(128)
+    rng = np.random.default_rng(128)
+    B, hq, hkv, d = 128, 32, 8, 128
+    lens = rng.integers(0, 401, size=B)
+    lens[::9] = 0
+    maxp = -(-int(lens.max()) // 16)
+    NB = sum(-(-int(n) // 16) for n in lens) + 8
+    cache = torch.randn((NB, 2, 16, hkv, d), device="cuda", dtype=torch.float16)
+    lengths = lens.astype(np.int32)
+    perm = rng.permutation(NB).astype(np.int32)
+    pages = np.full((B, maxp), -1, dtype=np.int32)
+    cur = 0
+    for i, n in enumerate(lens):
+        c = -(-int(n) // 16)
+        pages[i, :c] = perm[cur:cur + c]
+        cur += c
+    q = rng.standard_normal((B, hq, d)).astype(np.float16)
+    strides = (cache.stride(0), cache.stride(3), cache.stride(2), cache.stride(1))
+    scale = 1 / math.sqrt(d)
+    assert G.lib().bc_packed_decode_workspace_size(capi.Shape(B, hq, hkv, d, maxp, NB)) > 0
+    exp32, _ = oracle.packed_decode(q, cache.cpu().numpy(), pages, lengths, strides, hkv,
+                                    scale, threads=16)
+    for ws in (True, False):
+        out = G.packed(q, cache, strides, hkv, NB, pages, lengths, scale, workspace=ws)
+        err = np.abs(out.astype(np.float32) - exp32)
+        assert np.all(err <= G.f16_tolerance(exp32, 2e-3)), f"ws={ws} max err {err.max():.3e}"
+
+
 def test_misaligned_workspace_runs_unsplit():
     """A workspace that is not 16-byte aligned is ignored: the call gives the
     same bits as the call without one."""
