@@ -172,10 +172,12 @@ int bc_packed_decode(bc_shape shape, const bc_half* q, const bc_half* packed_kv,
                      long long head_stride, long long slot_stride,
                      long long kv_stride, float scale, bc_stream_t stream);
 
-/* Bytes of workspace bc_packed_decode_ws needs for this shape.  0 when the
- * page table holds at most 1024 tokens (max_pages * 16) and one workgroup per
- * (sequence, head block) fits the CUs: such calls run unsplit, with no merge,
- * whatever workspace is passed (the bc_auto_splits rule, from the shape only). */
+/* Bytes of workspace bc_packed_decode_ws needs for this shape.  0 when
+ * bc_auto_splits, given the table's capacity (max_pages * 16 tokens), keeps
+ * the shape unsplit: a table of at most 1024 tokens whose (sequence, head
+ * block) workgroups fit the CUs, or a batch above two waves of flat ranges
+ * (256 sequences at 8 KV heads on 256 CUs).  Such calls run unsplit, with no
+ * merge, whatever workspace is passed. */
 size_t bc_packed_decode_workspace_size(bc_shape shape);
 
 /* bc_packed_decode with the batch's pages spread over equal ranges of the
