@@ -454,6 +454,296 @@ __global__ __launch_bounds__(kThreads, 2) void tree_kernel(TreeParams P) {
   }
 }
 
+// Row-sharing variant for trees of four or more row tiles per (request, KV
+// head), where tree_kernel would read the prefix once per row tile: the four
+// waves take four row tiles and walk the same 32-token tiles, which the
+// workgroup loads once (two 16-byte chunks of K and of V per thread) into a
+// double-buffered LDS tile, one barrier per tile.  Each wave reads K back in
+// the A-operand layout and V through transpose reads, and owns its rows to
+// the end: no merge between waves.  Masks, softmax and the P.V product are
+// those of tree_kernel.
+template <int D>
+__global__ __launch_bounds__(kThreads, 2) void tree_rows_kernel(TreeParams P) {
+  constexpr int KS = D / 16;
+  constexpr int DT = D / 32;
+  constexpr int VP = v_pitch<D>();
+  constexpr int KP = D + 8;            // halves per staged K row
+  constexpr int CPR = D / 8;           // 16-byte chunks per token row
+  constexpr int CPT = kTile * CPR / kThreads;  // chunks per thread, K and V each
+  static_assert(CPT * kThreads == kTile * CPR, "tile chunks split evenly");
+  constexpr int BUF = kTile * (KP + VP);       // halves per staged tile
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int g = lane >> 5;
+  const int lr = lane & 31;
+
+  const int rgroups = (P.row_tiles + kWaves - 1) / kWaves;
+  const int zdim = P.hkv * rgroups;
+  const int z = blockIdx.x % zdim;
+  const int b = (blockIdx.x / zdim) % P.batch;
+  const int part = blockIdx.x / (zdim * P.batch);
+  const int kvh = z / rgroups;
+  const int rt = (z % rgroups) * kWaves + wave;  // row tile; idle when >= row_tiles
+
+  const int len = max(0, min(P.lengths[b], P.max_pages * BC_PAGE_SIZE));
+  int pbeg = 0, pend = len;
+  bool drafts = true, final_out = true;
+  if (P.part_acc) {
+    const int nparts = (len + P.chunk_tokens - 1) / P.chunk_tokens;
+    if (part < P.prefix_parts) {
+      if (part >= nparts) return;  // uniform over the workgroup
+      pbeg = part * P.chunk_tokens;
+      pend = min(pbeg + P.chunk_tokens, len);
+      drafts = false;
+    } else {
+      pend = 0;
+    }
+    final_out = nparts == 0;
+  }
+  const int tp0 = pbeg / kTile;
+  const int ntile_p = pend > pbeg ? (pend - 1) / kTile - tp0 + 1 : 0;
+  const int ntile = ntile_p + (drafts ? (P.nodes + kTile - 1) / kTile : 0);
+
+  const int r = rt * 32 + lr;
+  const bool rvalid = rt < P.row_tiles && r < P.rows;
+  const int node = rvalid ? r / P.group : 0;
+  const int h = kvh * P.group + (rvalid ? r % P.group : 0);
+
+  __shared__ int s_parent[BC_MAX_TREE_NODES];
+  __shared__ __attribute__((aligned(16))) _Float16 s_kv[2 * BUF];
+  __shared__ bool s_pok[2][2];
+
+  // Q^T B operand of this wave's row tile; parent entries (one per thread).
+  uint4 qB[KS];
+  {
+    const uint16_t* qp = P.dq + (((size_t)b * P.nodes + node) * P.hq + h) * D + 8 * g;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) qB[s] = rvalid ? ldg16(qp + 16 * s) : make_uint4(0, 0, 0, 0);
+  }
+  static_assert(BC_MAX_TREE_NODES <= kThreads, "one parent entry per thread");
+  const bool has_parent = (int)threadIdx.x < P.nodes;
+  const int par = P.parent[(size_t)b * P.nodes + min((int)threadIdx.x, P.nodes - 1)];
+
+  const size_t tok_stride = (size_t)P.hkv * D;
+  // Tile i's chunk c of this thread: token row c / CPR, dims 8 * (c % CPR).
+  // Every address stays inside its tensor: rows of invalid pages read page
+  // 0, draft rows past the node count read the last node; their V is staged
+  // as zeros and their scores are masked.
+  uint4 kreg[2][CPT], vreg[2][CPT];
+  bool vok[2][CPT];
+  int ph[2][2] = {{-1, -1}, {-1, -1}};
+  auto page_ids = [&](int i, int (&pg)[2]) {
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int pi = (tp0 + i) * (kTile / BC_PAGE_SIZE) + q;
+      pg[q] = i < ntile_p && pi < P.max_pages ? P.pages[(size_t)b * P.max_pages + pi] : -1;
+    }
+  };
+  auto load_tile = [&](int i, int set) {
+    const int (&pg)[2] = ph[set];
+    const bool is_draft = i >= ntile_p;
+    const int tbase = is_draft ? (i - ntile_p) * kTile : (tp0 + i) * kTile;
+#pragma unroll
+    for (int c = 0; c < CPT; ++c) {
+      const int chunk = (int)threadIdx.x + kThreads * c;
+      const int row = chunk / CPR, col = 8 * (chunk % CPR);
+      size_t off;
+      bool ok;
+      if (!is_draft) {
+        const int pgq = pg[row / BC_PAGE_SIZE];
+        const bool pok = pgq >= 0 && pgq < P.phys_pages;
+        const int t = tbase + row;
+        ok = pok && t >= pbeg && t < pend;
+        off = (pok ? ((size_t)pgq * BC_PAGE_SIZE + row % BC_PAGE_SIZE) * tok_stride : 0) +
+              (size_t)kvh * D + col;
+        kreg[set][c] = ldg16(P.k + off);
+        vreg[set][c] = ldg16(P.v + off);
+      } else {
+        const int dn = tbase + row;
+        ok = dn < P.nodes;
+        off = (((size_t)b * P.nodes + min(dn, P.nodes - 1)) * P.hkv + kvh) * D + col;
+        kreg[set][c] = ldg16(P.dk + off);
+        vreg[set][c] = ldg16(P.dv + off);
+      }
+      vok[set][c] = ok;
+    }
+  };
+  auto store_tile = [&](int i, int set) {
+    const int buf = i & 1;
+    const int (&pg)[2] = ph[set];
+    _Float16* sk = s_kv + buf * BUF;
+    _Float16* sv = sk + kTile * KP;
+#pragma unroll
+    for (int c = 0; c < CPT; ++c) {
+      const int chunk = (int)threadIdx.x + kThreads * c;
+      const int row = chunk / CPR, col = 8 * (chunk % CPR);
+      *reinterpret_cast<uint4*>(sk + row * KP + col) = kreg[set][c];
+      *reinterpret_cast<uint4*>(sv + row * VP + col) =
+          vok[set][c] ? vreg[set][c] : make_uint4(0, 0, 0, 0);
+    }
+    if (threadIdx.x < 2) {
+      const int pgq = pg[threadIdx.x];
+      s_pok[buf][threadIdx.x] = i >= ntile_p || (pgq >= 0 && pgq < P.phys_pages);
+    }
+  };
+
+  f32x16 acc[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+    for (int j = 0; j < 16; ++j) acc[dt][j] = 0.f;
+  float m = kNegInf, l = 0.f;
+  // Transpose-read address of this lane in a staged V tile.
+  const int trG = lane >> 4, trj = lane & 15;
+  const int vtr_off = (4 * (trG >> 1) + (trj >> 2)) * VP + 16 * (trG & 1) + 4 * (trj & 3);
+
+  auto compute = [&](int i, int buf) {
+    const _Float16* sk = s_kv + buf * BUF;
+    const _Float16* sv = sk + kTile * KP;
+    const bool is_draft = i >= ntile_p;
+    const int tbase = is_draft ? (i - ntile_p) * kTile : (tp0 + i) * kTile;
+    uint32_t okbits;
+    if (!is_draft) {
+      const int lo = min(max(pbeg - tbase, 0), kTile);
+      const int hi = min(max(pend - tbase, 0), kTile);
+      const uint32_t below_hi = hi >= kTile ? ~0u : (1u << hi) - 1u;
+      const uint32_t below_lo = lo >= kTile ? ~0u : (1u << lo) - 1u;
+      okbits = (below_hi & ~below_lo) &
+               ((s_pok[buf][0] ? 0x0000ffffu : 0u) | (s_pok[buf][1] ? 0xffff0000u : 0u));
+    } else {
+      okbits = 0;
+      int cur = node;
+      for (int steps = 0; steps < P.nodes && cur >= 0 && cur < P.nodes; ++steps) {
+        if (cur >= tbase && cur < tbase + kTile) okbits |= 1u << (cur - tbase);
+        cur = s_parent[cur];
+      }
+    }
+    // ---- S^T = K Q^T, K from the staged tile in the A-operand layout ----
+    f32x16 sc;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) sc[j] = 0.f;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      const uint4 ka = *reinterpret_cast<const uint4*>(sk + lr * KP + 16 * s + 8 * g);
+      sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_f16x8(ka), as_f16x8(qB[s]), sc, 0, 0, 0);
+    }
+    // ---- mask and online softmax (column lr = query row) ----
+    const uint32_t ob = okbits >> (4 * g);
+    float svv[16];
+    float tmax = kNegInf;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const bool ok = (ob >> (8 * (j >> 2) + (j & 3))) & 1u;
+      svv[j] = ok ? sc[j] * P.scale_log2 : kNegInf;
+      tmax = __builtin_fmaxf(tmax, svv[j]);
+    }
+    tmax = __builtin_fmaxf(tmax, shfl_xor_f(tmax, 32));
+    const float mnew = __builtin_fmaxf(m, tmax);
+    if (__builtin_amdgcn_ballot_w64(mnew > m + kRescaleSlack)) {
+      const float alpha = fast_exp2(m - safe_max(mnew));
+      l *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) acc[dt][j] *= alpha;
+      m = mnew;
+    }
+    const float mb = safe_max(m);
+    f16x8 pb[2], pl[2];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const float pr = fast_exp2(svv[j] - mb);
+      l += pr;
+      const _Float16 hi = (_Float16)pr;
+      pb[j >> 3][j & 7] = hi;
+      pl[j >> 3][j & 7] = (_Float16)(pr - (float)hi);
+    }
+    // ---- O^T += V^T P^T from the staged tile ----
+    const _Float16* vtr = sv + vtr_off;
+    f16x8 av[DT][2];
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int st = 0; st < 2; ++st) {
+        const f16x4 lo = lds_read_tr(vtr + (16 * st) * VP + 32 * dt);
+        const f16x4 hi = lds_read_tr(vtr + (16 * st + 8) * VP + 32 * dt);
+        av[dt][st] = f16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      }
+#pragma unroll
+    for (int st = 0; st < 2; ++st)
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+        acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[dt][st], pb[st], acc[dt], 0, 0, 0);
+#pragma unroll
+    for (int st = 0; st < 2; ++st)
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+        acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[dt][st], pl[st], acc[dt], 0, 0, 0);
+  };
+
+  // Loads run two tiles ahead in two register sets (set = tile & 1); LDS
+  // holds two staged tiles (buffer = tile & 1).  Tiles 0 and 1 are loaded
+  // and tile 0 staged before the first barrier, together with the parent
+  // array.  Step i loads tile i + 2, computes tile i and stages tile i + 1,
+  // then the barrier publishes tile i + 1 and frees tile i's buffer.
+  if (ntile > 0) {
+    page_ids(0, ph[0]);
+    load_tile(0, 0);
+  }
+  if (ntile > 1) {
+    page_ids(1, ph[1]);
+    load_tile(1, 1);
+  }
+  if (ntile > 0) store_tile(0, 0);
+  if (has_parent) s_parent[threadIdx.x] = par;
+  __syncthreads();
+  auto step = [&](int i, int set) {  // set = i & 1, a compile-time constant
+    if (i >= ntile) return;
+    if (i + 2 < ntile) {
+      page_ids(i + 2, ph[set]);
+      load_tile(i + 2, set);
+    }
+    if (rt < P.row_tiles) compute(i, set);
+    if (i + 1 < ntile) store_tile(i + 1, set ^ 1);
+    __syncthreads();
+  };
+  for (int i = 0; i < ntile; i += 2) {
+    step(i, 0);
+    step(i + 1, 1);
+  }
+  if (!rvalid) return;
+  l += shfl_xor_f(l, 32);
+
+  // ---- write: lane holds O^T[32dt + 8jq + 4g + e][row r] ----
+  if (final_out) {
+    float* dst = P.out + (((size_t)b * P.nodes + node) * P.hq + h) * D;
+    const float inv = 1.f / l;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int jq = 0; jq < 4; ++jq)
+        *reinterpret_cast<float4*>(dst + 32 * dt + 8 * jq + 4 * g) =
+            make_float4(acc[dt][4 * jq] * inv, acc[dt][4 * jq + 1] * inv,
+                        acc[dt][4 * jq + 2] * inv, acc[dt][4 * jq + 3] * inv);
+  } else {
+    const int p = drafts ? P.prefix_parts : part;
+    const size_t slot = slot_index(P, b, node, h, p);
+    float* dst = P.part_acc + slot * D;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int jq = 0; jq < 4; ++jq)
+        *reinterpret_cast<float4*>(dst + 32 * dt + 8 * jq + 4 * g) =
+            make_float4(acc[dt][4 * jq], acc[dt][4 * jq + 1], acc[dt][4 * jq + 2],
+                        acc[dt][4 * jq + 3]);
+    if (g == 0) {
+      P.part_ml[2 * slot] = m;
+      P.part_ml[2 * slot + 1] = l;
+    }
+  }
+}
+
 // Combines the prefix chunks and the draft part of every (b, node, h): one
 // wave per output row, lane p reads slot p's (max, sum), the weights are
 // formed once and every lane accumulates its dims with independent loads.
@@ -559,19 +849,41 @@ TreeParams make_params(const bc_shape& s, const bc_tree_inputs& in, int nodes) {
 // both measured slower at 8 x 2053 tokens (22.7 against 20.9 us): each
 // workgroup's fixed start, merge and partial-write cost outweighs the
 // second wave per SIMD.
+// tree_rows_kernel (one K/V tile shared by four row tiles) pays once
+// tree_kernel would run two or more workgroups per CU reading the prefix
+// once per row tile: at 8 requests of a 2048-token prefix, 64 nodes took 64
+// against 69 us and 256 nodes 164 against 273 us.  With fewer row tiles, or
+// without a workspace and fewer row groups than CUs, its serial walk over
+// the tiles lost (one request, 32 nodes, no workspace: 101 against 36 us).
+bool rows_kernel_for(int batch, int hkv, int row_tiles, bool workspace, int cus) {
+  if (row_tiles < kWaves) return false;
+  if ((long long)batch * hkv * row_tiles < 2LL * cus) return false;
+  return workspace ||
+         (long long)batch * hkv * ((row_tiles + kWaves - 1) / kWaves) >= cus;
+}
+
+// Workgroups per (request, KV head, prefix chunk).
+int row_units(int row_tiles, bool rows_kernel) {
+  return rows_kernel ? (row_tiles + kWaves - 1) / kWaves : row_tiles;
+}
+
 void tree_chunking(const bc_shape& s, int nodes, int* chunk_tokens, int* parts) {
   const int group = s.query_heads / s.kv_heads;
-  const long long units =
-      (long long)s.batch * s.kv_heads * ((nodes * group + 31) / 32);
-  const int max_tokens = s.max_pages * BC_PAGE_SIZE;
+  const int row_tiles = (nodes * group + 31) / 32;
   const int cus = bch::device_cus();
-  long long want = cus / units - 1;
-  // With units in (cus/3, cus/2] the rule above gives a single chunk, which
-  // leaves half or more of the CUs idle while each workgroup walks the whole
-  // prefix; two chunks plus the draft part keep every workgroup resident (two
-  // per CU) and measured 25-26 us against 35 us at 12 and 16 requests of a
-  // 2048-token prefix.  More units than that measured slower with two.
-  if (want < 2 && 2LL * units <= cus) want = 2;
+  const bool rows = rows_kernel_for(s.batch, s.kv_heads, row_tiles, true, cus);
+  const long long units = (long long)s.batch * s.kv_heads * row_units(row_tiles, rows);
+  const int max_tokens = s.max_pages * BC_PAGE_SIZE;
+  // tree_rows_kernel walks its tiles in series, so it takes two workgroups
+  // per CU (two fit); tree_kernel's four waves split the tiles, one per CU.
+  long long want = (rows ? 2LL * cus : cus) / units - 1;
+  // With units in (cus/3, cus/2] the rule above gives tree_kernel a single
+  // chunk, which leaves half or more of the CUs idle while each workgroup
+  // walks the whole prefix; two chunks plus the draft part keep every
+  // workgroup resident (two per CU) and measured 25-26 us against 35 us at
+  // 12 and 16 requests of a 2048-token prefix.  More units than that
+  // measured slower with two.
+  if (!rows && want < 2 && 2LL * units <= cus) want = 2;
   if (want < 1) want = 1;
   int chunk = (int)((max_tokens + want - 1) / want);
   chunk = (chunk + kTile - 1) / kTile * kTile;
@@ -592,9 +904,17 @@ size_t tree_workspace(const bc_shape& s, int nodes, int* chunk_tokens, int* part
 }
 
 hipError_t launch_tree(TreeParams& P, int dim, int parts, hipStream_t st) {
-  const dim3 grid((unsigned)((size_t)parts * P.batch * P.hkv * P.row_tiles));
-  if (dim == 64) tree_kernel<64><<<grid, kThreads, 0, st>>>(P);
-  else tree_kernel<128><<<grid, kThreads, 0, st>>>(P);
+  const bool rows_kernel = rows_kernel_for(P.batch, P.hkv, P.row_tiles, P.part_acc != nullptr,
+                                           bch::device_cus());
+  const dim3 grid(
+      (unsigned)((size_t)parts * P.batch * P.hkv * row_units(P.row_tiles, rows_kernel)));
+  if (rows_kernel) {
+    if (dim == 64) tree_rows_kernel<64><<<grid, kThreads, 0, st>>>(P);
+    else tree_rows_kernel<128><<<grid, kThreads, 0, st>>>(P);
+  } else {
+    if (dim == 64) tree_kernel<64><<<grid, kThreads, 0, st>>>(P);
+    else tree_kernel<128><<<grid, kThreads, 0, st>>>(P);
+  }
   hipError_t err = hipGetLastError();
   if (err != hipSuccess || !P.part_acc) return err;
   const size_t rows = (size_t)P.batch * P.nodes * P.hq;
