@@ -31,6 +31,9 @@
 // LDS; with a workspace, chunks write FP32 partials that merge_tree_kernel
 // combines.  Workgroup ids put (KV head, row tile) in the low bits, so the
 // requests that share prefix pages run on the same XCD and reuse its L2.
+// Large trees, whose row tiles would need two or more such workgroups per
+// CU, run tree_rows_kernel instead: its unit is (request, KV head, four row
+// tiles, prefix chunk), and each K/V tile is loaded once for all four.
 #include "bc_device.h"
 #include "bc_host.h"
 
