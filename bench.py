@@ -53,7 +53,8 @@ def parse():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
-    ap.add_argument("--only", default="", help="comma list of configs to run (c1..c5)")
+    ap.add_argument("--only", default="",
+                    help="comma list of configs to run (c1..c5; tl = a 256-node tree)")
     ap.add_argument("--calibrate", action="store_true",
                     help="also run a plain 512 MiB device copy, the known-size reference "
                          "for scaling FETCH_SIZE / WRITE_SIZE counters")
@@ -306,12 +307,12 @@ def bench_c5_paged(cx, c5):
     return res
 
 
-def tree_setup(cx, batch, prefix, seed):
+def tree_setup(cx, batch, prefix, seed, nodes=7):
     """Shared-prefix tree fixture on the GPU: every request's page-table row
     names the same physical pages (random permutation of the pool)."""
     t = cx.torch
     rng = np.random.default_rng(seed)
-    hq, hkv, d, n = 32, 8, 128, 7
+    hq, hkv, d, n = 32, 8, 128, nodes
     npg = -(-prefix // PAGE)
     pool = npg + 2 * batch + 2
     perm = rng.permutation(pool).astype(np.int32)
@@ -411,9 +412,9 @@ def expanded_fixture(cx, f):
             t.tensor(lens, device="cuda", dtype=t.int32), lens)
 
 
-def bench_tree(cx, batch, prefix, seed, with_expanded):
+def bench_tree(cx, batch, prefix, seed, with_expanded, nodes=7):
     t = cx.torch
-    f = tree_setup(cx, batch, prefix, seed)
+    f = tree_setup(cx, batch, prefix, seed, nodes)
     res = {}
     calls = {"ws": tree_call(cx, f, True), "single": tree_call(cx, f, False)}
     outs = {}
@@ -454,7 +455,7 @@ def bench_tree(cx, batch, prefix, seed, with_expanded):
                    expanded_over_tree=round(exp_us / tree_us, 2))
         del ek, ev
         res["commit"] = bench_commit(cx, f)
-    res["workload"] = (f"tree_verify {batch} req x {prefix} shared prefix + 7 nodes "
+    res["workload"] = (f"tree_verify {batch} req x {prefix} shared prefix + {nodes} nodes "
                        "(random parents), Hq=32 Hkv=8 D=128")
     return res
 
@@ -605,6 +606,13 @@ def main():
     if want("c3"):
         results["c3_tree"] = bench_tree(cx, 8, 2053, 3, with_expanded=True)
         print(f"[bench] C3 {results['c3_tree']}", file=sys.stderr, flush=True)
+    if want("tl"):
+        # A large draft tree (beyond the benchmark configs): 8 requests x 256
+        # nodes over a 2048-token shared prefix, where the verifier shares each
+        # K/V tile between four row tiles.
+        results["tree_large"] = bench_tree(cx, 8, 2048, 4, with_expanded=False, nodes=256)
+        print(f"[bench] tree 8 x 2048 x 256 nodes {results['tree_large']}", file=sys.stderr,
+              flush=True)
     if want("c4"):
         results["c4_decode"] = bench_c4(cx)
         print(f"[bench] C4 {results['c4_decode']}", file=sys.stderr, flush=True)
