@@ -40,9 +40,9 @@ sys.path.insert(0, str(ROOT / "branchcraft-cuda_amd" / "python"))
 
 HBM_PEAK_GBS = 8000.0
 # HBM bytes per config-5 call measured with rocprofv3 counters: attention
-# FETCH 265,212.4 KiB x 2 + WRITE 5,028.8 KiB, merge FETCH 2,636.0 KiB x 2 +
+# FETCH 265,215.5 KiB x 2 + WRITE 5,028.8 KiB, merge FETCH 2,636.0 KiB x 2 +
 # WRITE 472.0 KiB (FETCH_SIZE reads half of a 512 MiB copy's bytes).
-C5_HBM_TRAFFIC_BYTES = (265212.4 * 2 + 5028.8 + 2636.0 * 2 + 472.0) * 1024
+C5_HBM_TRAFFIC_BYTES = (265215.5 * 2 + 5028.8 + 2636.0 * 2 + 472.0) * 1024
 MFMA_F16_PEAK_TFLOPS = 2500.0
 PAGE = 16
 
