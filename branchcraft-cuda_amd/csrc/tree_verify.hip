@@ -750,6 +750,12 @@ __global__ __launch_bounds__(kThreads, 2) void tree_rows_kernel(TreeParams P) {
 // Combines the prefix chunks and the draft part of every (b, node, h): one
 // wave per output row, lane p reads slot p's (max, sum), the weights are
 // formed once and every lane accumulates its dims with independent loads.
+// Slot p < prefix_parts holds prefix chunk p, slot prefix_parts the draft
+// part.  The request's length only says how many prefix slots were written
+// (nparts), so the (max, sum) of every slot, the draft slot's accumulator
+// and the first eight prefix slots' go out together with the length, and
+// unwritten slots are masked afterwards by selects (their contents are
+// whatever the workspace held, NaN included).
 template <int D>
 __global__ __launch_bounds__(256) void merge_tree_kernel(TreeParams P) {
   constexpr int PER = D / 64;
@@ -757,50 +763,55 @@ __global__ __launch_bounds__(256) void merge_tree_kernel(TreeParams P) {
   const size_t row = (size_t)blockIdx.x * 4 + (threadIdx.x >> 6);  // (b*N+node)*Hq+h
   if (row >= (size_t)P.batch * P.nodes * P.hq) return;
   const int b = row / ((size_t)P.nodes * P.hq);
-  const int len = max(0, min(P.lengths[b], P.max_pages * BC_PAGE_SIZE));
+  const int lraw = P.lengths[b];
+  const int dslot = P.prefix_parts;  // 2 <= prefix_parts <= 63 (tree_chunking)
+  const size_t base = row * (P.prefix_parts + 1);
+  auto load_slot = [&](int sidx, float (&v)[PER]) {
+    const float* src = P.part_acc + (base + sidx) * D + lane;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) v[j] = src[64 * j];
+  };
+  const size_t ms = base + min(lane, dslot);
+  const float mp0 = P.part_ml[2 * ms], lp0 = P.part_ml[2 * ms + 1];
+  float vd[PER], v[8][PER];
+  load_slot(dslot, vd);
+#pragma unroll
+  for (int u = 0; u < 8; ++u) load_slot(min(u, dslot - 1), v[u]);
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    asm volatile("" ::"v"(vd[j]));
+#pragma unroll
+    for (int u = 0; u < 8; ++u) asm volatile("" ::"v"(v[u][j]));
+  }
+  const int len = max(0, min(lraw, P.max_pages * BC_PAGE_SIZE));
   const int nparts = (len + P.chunk_tokens - 1) / P.chunk_tokens;
   if (nparts == 0) return;  // the draft part wrote the final output
-  const size_t base = row * (P.prefix_parts + 1);
-  // slot of part i: prefix chunks 0..nparts-1, then the draft slot
-  auto slot = [&](int i) { return base + (i == nparts ? P.prefix_parts : i); };
-  // Eight parts per step, all loads issued before the first use; steps past
-  // the last part re-read it with weight 0 (lanes past nparts hold w = 0).
-  auto load8p = [&](int i0, float (&v)[8][PER]) {
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const float* src = P.part_acc + slot(min(i0 + u, nparts)) * D + lane;
-#pragma unroll
-      for (int j = 0; j < PER; ++j) v[u][j] = src[64 * j];
-    }
-  };
-  // Every part's (max, sum) (nparts < 64 is guaranteed by tree_chunking) and
-  // the first eight parts' accumulators go out together, one wait for both:
-  // left alone, the compiler sinks the accumulator loads below the
-  // reductions and pays a second round trip.
-  const size_t ms = slot(min(lane, nparts));
-  const float mp0 = P.part_ml[2 * ms], lp0 = P.part_ml[2 * ms + 1];
-  float v[8][PER];
-  load8p(0, v);
-#pragma unroll
-  for (int u = 0; u < 8; ++u)
-#pragma unroll
-    for (int j = 0; j < PER; ++j) asm volatile("" ::"v"(v[u][j]));
-  const float mp = lane <= nparts ? mp0 : kNegInf;
-  const float lp = lane <= nparts ? lp0 : 0.f;
+  const bool written = lane < nparts || lane == dslot;
+  const float mp = written ? mp0 : kNegInf;
+  const float lp = written ? lp0 : 0.f;
   const float mm = wave_max(mp);
   const float w = fast_exp2(mp - mm);  // every row sees its own node: mm finite
   const float lsum = wave_sum(w * lp);
+  auto weight = [&](int sidx) {
+    return __builtin_bit_cast(float,
+                              __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), sidx));
+  };
   float a[PER];
+  const float wd = weight(dslot);
 #pragma unroll
-  for (int j = 0; j < PER; ++j) a[j] = 0.f;
-  for (int i0 = 0; i0 <= nparts; i0 += 8) {
-    if (i0 > 0) load8p(i0, v);
+  for (int j = 0; j < PER; ++j) a[j] = wd * vd[j];
+  for (int i0 = 0; i0 < nparts; i0 += 8) {
+    if (i0 > 0) {
+#pragma unroll
+      for (int u = 0; u < 8; ++u) load_slot(min(i0 + u, nparts - 1), v[u]);
+    }
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
-      const float wi = __builtin_bit_cast(
-          float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), min(i0 + u, 63)));
+      if (i0 + u < nparts) {  // uniform
+        const float wi = weight(i0 + u);
 #pragma unroll
-      for (int j = 0; j < PER; ++j) a[j] += wi * v[u][j];
+        for (int j = 0; j < PER; ++j) a[j] += wi * v[u][j];
+      }
     }
   }
   const float inv = 1.f / lsum;
