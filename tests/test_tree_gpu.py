@@ -128,6 +128,65 @@ def test_large_trees_share_tiles_across_row_tiles(batch, nodes, hq, hkv, d, orac
     _check(fix, oracle, atol=3e-4, what=f"B={batch} N={nodes} D={d}")
 
 
+def _group_fixture(rng, lengths, share, nodes=7, hq=32, hkv=8, d=128, cow_last=(),
+                   extra_pages=1):
+    """Per-request prefixes over one page pool.  Request i reuses request
+    share[i]'s page ids (share[i] < i) over the pages both cover and takes
+    fresh pages beyond; share[i] = -1 gives it fresh pages throughout.
+    Requests in `cow_last` then get a fresh last page, as a copy-on-write
+    commit leaves them."""
+    lengths = np.asarray(lengths, dtype=np.int32)
+    batch = len(lengths)
+    npg = [-(-int(x) // 16) for x in lengths]
+    max_pages = max(max(npg), 1) + extra_pages
+    pool = sum(npg) + len(cow_last) + 8
+    _, k, v, _, _ = oracle_np.paged_fixture(rng, 1, hq, hkv, d, [16], pool=pool, sigma=1.0)
+    fresh = iter(rng.permutation(pool).astype(np.int32))
+    pages = np.full((batch, max_pages), -1, dtype=np.int32)
+    for i in range(batch):
+        j = share[i]
+        for p in range(npg[i]):
+            pages[i, p] = pages[j, p] if j >= 0 and p < npg[j] else next(fresh)
+        if i in cow_last and npg[i] > 0:
+            pages[i, npg[i] - 1] = next(fresh)
+    dq = rng.standard_normal((batch, nodes, hq, d)).astype(np.float16)
+    dk = rng.standard_normal((batch, nodes, hkv, d)).astype(np.float16)
+    dv = rng.standard_normal((batch, nodes, hkv, d)).astype(np.float16)
+    par = oracle_np.random_parents(rng, batch, nodes)
+    return k, v, pages, lengths, dq, dk, dv, par
+
+
+@pytest.mark.parametrize("case", [
+    # every request on its own pages
+    dict(lengths=[611, 95, 870, 402, 333, 777, 128, 640], share=[-1] * 8),
+    # requests 1-3 share request 0's pages, request 3 ending early; 5 and 6
+    # share request 4's, request 5 with a copied last page
+    dict(lengths=[613, 613, 613, 400, 613, 613, 613], share=[-1, 0, 0, 0, -1, 4, 4],
+         cow_last=(5,)),
+    # five requests on one page table
+    dict(lengths=[300] * 5, share=[-1, 0, 0, 0, 0]),
+    # an empty request beside three sharing ones (its drafts give the output)
+    dict(lengths=[300, 0, 300, 300], share=[-1, 0, 0, 0]),
+    # page tables far longer than every request (empty prefix chunks)
+    dict(lengths=[100, 100, 100], share=[-1, 0, 0], extra_pages=38),
+    # two requests; D = 64, group 4, eight nodes (32 rows)
+    dict(lengths=[517, 517], share=[-1, 0], nodes=8, hq=8, hkv=2, d=64),
+    # group 1: 32 nodes fill the row tile and the draft tile
+    dict(lengths=[290, 290, 290, 290], share=[-1, 0, 0, 0], nodes=32, hq=8, hkv=8),
+])
+def test_per_request_page_tables(case, oracle):
+    """Requests whose page tables share some pages and not others, end at
+    different lengths, hold a copied last page or are empty, with and
+    without a workspace."""
+    rng = np.random.default_rng(len(case["lengths"]) * 7 + sum(case["lengths"]))
+    fix = _group_fixture(rng, **case)
+    k, v, pages, lengths, dq, dk, dv, par = fix
+    b, n, hq, d = dq.shape
+    shape = capi.Shape(b, hq, k.shape[2], d, pages.shape[1], k.shape[0])
+    assert G.lib().bc_tree_verify_workspace_size(shape, n) > 0
+    _check(fix, oracle, atol=3e-4, what=str(case))
+
+
 def test_misaligned_workspace_runs_single_pass():
     """A workspace that is not 16-byte aligned is ignored: the call gives the
     same bits as bc_tree_verify."""
