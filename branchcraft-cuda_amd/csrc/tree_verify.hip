@@ -34,6 +34,9 @@
 // Large trees, whose row tiles would need two or more such workgroups per
 // CU, run tree_rows_kernel instead: its unit is (request, KV head, four row
 // tiles, prefix chunk), and each K/V tile is loaded once for all four.
+// bc_tree_verify_shared_ws, for requests forked from one prefix, runs
+// tree_group_kernel: its unit is (four requests, KV head, prefix chunk), and
+// each tile is loaded once for the four requests where their pages agree.
 #include "bc_device.h"
 #include "bc_host.h"
 
@@ -747,6 +750,374 @@ __global__ __launch_bounds__(kThreads, 2) void tree_rows_kernel(TreeParams P) {
   }
 }
 
+// Request-group variant for trees of one row tile per (request, KV head),
+// workspace path only.  The four waves take four requests of one KV head and
+// one prefix chunk.  When the requests' page ids over the chunk and their
+// chunk ends agree -- requests forked from one prefix -- the workgroup loads
+// each 32-token tile once into LDS for all four (the tree_rows_kernel
+// pipeline: two 16-byte chunks of K and of V per thread, two tiles ahead,
+// one barrier per tile), so a CU reads the shared prefix once per four
+// requests instead of once per request.  Otherwise, and for the draft part,
+// every wave walks its own request's tiles with its own loads (eight chunks
+// of K and of V per lane, one tile ahead) through its own LDS tile.  Masks,
+// softmax and the P.V product are those of tree_kernel.
+template <int D>
+__global__ __launch_bounds__(kThreads, 2) void tree_group_kernel(TreeParams P) {
+  constexpr int KS = D / 16;
+  constexpr int DT = D / 32;
+  constexpr int VP = v_pitch<D>();
+  constexpr int KP = D + 8;            // halves per staged K row
+  constexpr int CPR = D / 8;           // 16-byte chunks per token row
+  constexpr int CPT = kTile * CPR / kThreads;  // shared loads: chunks per thread
+  constexpr int CPL = kTile * CPR / 64;        // private loads: chunks per lane
+  static_assert(CPT * kThreads == kTile * CPR, "tile chunks split evenly");
+  constexpr int BUF = kTile * (KP + VP);       // halves per staged tile
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int g = lane >> 5;
+  const int lr = lane & 31;
+
+  const int ngroups = (P.batch + kWaves - 1) / kWaves;
+  const int kvh = blockIdx.x % P.hkv;
+  const int b0 = (blockIdx.x / P.hkv) % ngroups * kWaves;
+  const int part = blockIdx.x / (P.hkv * ngroups);
+  const int nact = min(kWaves, P.batch - b0);  // requests of this group
+  const bool active = wave < nact;
+  const int b = b0 + min(wave, nact - 1);
+  const bool drafts = part >= P.prefix_parts;
+  const int max_tokens = P.max_pages * BC_PAGE_SIZE;
+  const int pbeg = drafts ? 0 : part * P.chunk_tokens;
+
+  // Chunk ends of the group's requests (<= pbeg: no tiles in this chunk),
+  // and the page ids of the chunk compared against the first request's.
+  int pend[kWaves];
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) {
+    const int lw = max(0, min(P.lengths[b0 + min(w, nact - 1)], max_tokens));
+    pend[w] = drafts ? lw : min(pbeg + P.chunk_tokens, lw);
+  }
+  const int mylen = max(0, min(P.lengths[b], max_tokens));
+  // All of this goes out in one round: the page loads do not wait for the
+  // lengths, which only mask the comparison afterwards.
+  int mismatch = 0;
+  const int tp0 = pbeg / kTile;
+  int pg_b0[2] = {-1, -1}, pg_own[2] = {-1, -1};  // first tile's page ids
+  if (!drafts) {
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int pi = tp0 * (kTile / BC_PAGE_SIZE) + q;
+      if (pi < P.max_pages) {
+        pg_b0[q] = P.pages[(size_t)b0 * P.max_pages + pi];
+        pg_own[q] = P.pages[(size_t)b * P.max_pages + pi];
+      }
+    }
+    const int p0 = pbeg / BC_PAGE_SIZE;
+    const int np = (min(pbeg + P.chunk_tokens, max_tokens) - pbeg + BC_PAGE_SIZE - 1) /
+                   BC_PAGE_SIZE;
+    for (int j = threadIdx.x; j < np; j += kThreads) {
+      const int p = p0 + j;  // < max_pages: pbeg + 16 j < max_tokens
+      int id[kWaves];
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w)
+        id[w] = P.pages[(size_t)(b0 + min(w, nact - 1)) * P.max_pages + p];
+#pragma unroll
+      for (int w = 1; w < kWaves; ++w)
+        if (w < nact && p * BC_PAGE_SIZE < pend[0] && id[w] != id[0]) mismatch = 1;
+    }
+  }
+  bool same_end = true;
+#pragma unroll
+  for (int w = 1; w < kWaves; ++w) same_end = same_end && (w >= nact || pend[w] == pend[0]);
+
+  const int r = lr;
+  const bool rvalid = active && r < P.rows;
+  const int node = rvalid ? r / P.group : 0;
+  const int h = kvh * P.group + (rvalid ? r % P.group : 0);
+
+  __shared__ int s_parent[kWaves][32];
+  __shared__ __attribute__((aligned(16))) _Float16 s_kv[kWaves * BUF];
+  __shared__ bool s_pok[2][2];
+
+  uint4 qB[KS];
+  {
+    const uint16_t* qp = P.dq + (((size_t)b * P.nodes + node) * P.hq + h) * D + 8 * g;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) qB[s] = rvalid ? ldg16(qp + 16 * s) : make_uint4(0, 0, 0, 0);
+  }
+  if (drafts && lane < 32)
+    s_parent[wave][lane] = P.parent[(size_t)b * P.nodes + min(lane, P.nodes - 1)];
+
+  const size_t tok_stride = (size_t)P.hkv * D;
+  // Token row `row` of prefix page `pg` (page 0 for an invalid page, staged
+  // as zero V and masked) at dims col..col+7 of this KV head.
+  auto prefix_off = [&](int pg, int row, int col) {
+    const bool pok = pg >= 0 && pg < P.phys_pages;
+    return (pok ? ((size_t)pg * BC_PAGE_SIZE + row % BC_PAGE_SIZE) * tok_stride : 0) +
+           (size_t)kvh * D + col;
+  };
+  // Shared-mode registers: two sets, tile i in set i & 1.  Tile 0's loads
+  // (from the first request's page ids) go out before the barrier that
+  // decides the mode; a private-mode workgroup drops them.
+  uint4 kreg[2][CPT], vreg[2][CPT];
+  int ph[2][2] = {{pg_b0[0], pg_b0[1]}, {-1, -1}};
+  auto load_shared = [&](int i, int set) {
+    const int (&pg)[2] = ph[set];
+#pragma unroll
+    for (int c = 0; c < CPT; ++c) {
+      const int chunk = (int)threadIdx.x + kThreads * c;
+      const int row = chunk / CPR, col = 8 * (chunk % CPR);
+      const size_t off = prefix_off(pg[row / BC_PAGE_SIZE], row, col);
+      kreg[set][c] = ldg16(P.k + off);
+      vreg[set][c] = ldg16(P.v + off);
+    }
+  };
+  if (!drafts) load_shared(0, 0);
+  // Also the barrier that publishes the parent arrays.
+  const int any_mismatch = __syncthreads_or(mismatch);
+  const bool shared = !drafts && same_end && !any_mismatch;
+  if (!drafts && pend[0] <= pbeg && same_end) return;  // no request has tiles here
+  f32x16 acc[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+    for (int j = 0; j < 16; ++j) acc[dt][j] = 0.f;
+  float m = kNegInf, l = 0.f;
+  const int trG = lane >> 4, trj = lane & 15;
+  const int vtr_off = (4 * (trG >> 1) + (trj >> 2)) * VP + 16 * (trG & 1) + 4 * (trj & 3);
+
+  // Valid-token mask of prefix tile tbase for the range [pbeg, pe).
+  auto prefix_bits = [&](int tbase, int pe, bool pok0, bool pok1) {
+    const int lo = min(max(pbeg - tbase, 0), kTile);
+    const int hi = min(max(pe - tbase, 0), kTile);
+    const uint32_t below_hi = hi >= kTile ? ~0u : (1u << hi) - 1u;
+    const uint32_t below_lo = lo >= kTile ? ~0u : (1u << lo) - 1u;
+    return (below_hi & ~below_lo) & ((pok0 ? 0x0000ffffu : 0u) | (pok1 ? 0xffff0000u : 0u));
+  };
+  // Ancestor mask of draft tile tbase for this lane's node.
+  auto draft_bits = [&](int tbase) {
+    uint32_t bits = 0;
+    int cur = node;
+    for (int steps = 0; steps < P.nodes && cur >= 0 && cur < P.nodes; ++steps) {
+      if (cur >= tbase && cur < tbase + kTile) bits |= 1u << (cur - tbase);
+      cur = s_parent[wave][cur];
+    }
+    return bits;
+  };
+
+  auto compute = [&](const _Float16* sk, uint32_t okbits) {
+    const _Float16* sv = sk + kTile * KP;
+    f32x16 sc;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) sc[j] = 0.f;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      const uint4 ka = *reinterpret_cast<const uint4*>(sk + lr * KP + 16 * s + 8 * g);
+      sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_f16x8(ka), as_f16x8(qB[s]), sc, 0, 0, 0);
+    }
+    const uint32_t ob = okbits >> (4 * g);
+    float svv[16];
+    float tmax = kNegInf;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const bool ok = (ob >> (8 * (j >> 2) + (j & 3))) & 1u;
+      svv[j] = ok ? sc[j] * P.scale_log2 : kNegInf;
+      tmax = __builtin_fmaxf(tmax, svv[j]);
+    }
+    tmax = __builtin_fmaxf(tmax, shfl_xor_f(tmax, 32));
+    const float mnew = __builtin_fmaxf(m, tmax);
+    if (__builtin_amdgcn_ballot_w64(mnew > m + kRescaleSlack)) {
+      const float alpha = fast_exp2(m - safe_max(mnew));
+      l *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) acc[dt][j] *= alpha;
+      m = mnew;
+    }
+    const float mb = safe_max(m);
+    f16x8 pb[2], pl[2];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const float pr = fast_exp2(svv[j] - mb);
+      l += pr;
+      const _Float16 hi = (_Float16)pr;
+      pb[j >> 3][j & 7] = hi;
+      pl[j >> 3][j & 7] = (_Float16)(pr - (float)hi);
+    }
+    const _Float16* vtr = sv + vtr_off;
+    f16x8 av[DT][2];
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int st = 0; st < 2; ++st) {
+        const f16x4 lo = lds_read_tr(vtr + (16 * st) * VP + 32 * dt);
+        const f16x4 hi = lds_read_tr(vtr + (16 * st + 8) * VP + 32 * dt);
+        av[dt][st] = f16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      }
+#pragma unroll
+    for (int st = 0; st < 2; ++st)
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+        acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[dt][st], pb[st], acc[dt], 0, 0, 0);
+#pragma unroll
+    for (int st = 0; st < 2; ++st)
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+        acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[dt][st], pl[st], acc[dt], 0, 0, 0);
+  };
+
+  if (shared) {
+    // ---- one staged tile for every wave; range [pbeg, pend[0]) ----
+    const int pe = pend[0];
+    const int ntile = (pe - 1) / kTile - tp0 + 1;
+    auto page_ids = [&](int i, int (&pg)[2]) {
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const int pi = (tp0 + i) * (kTile / BC_PAGE_SIZE) + q;
+        pg[q] = pi < P.max_pages ? P.pages[(size_t)b0 * P.max_pages + pi] : -1;
+      }
+    };
+    auto store_tile = [&](int i, int set) {
+      const int buf = i & 1;
+      const int tbase = (tp0 + i) * kTile;
+      _Float16* sk = s_kv + buf * BUF;
+      _Float16* sv = sk + kTile * KP;
+#pragma unroll
+      for (int c = 0; c < CPT; ++c) {
+        const int chunk = (int)threadIdx.x + kThreads * c;
+        const int row = chunk / CPR, col = 8 * (chunk % CPR);
+        const int pgq = ph[set][row / BC_PAGE_SIZE];
+        const int t = tbase + row;
+        const bool ok = pgq >= 0 && pgq < P.phys_pages && t >= pbeg && t < pe;
+        *reinterpret_cast<uint4*>(sk + row * KP + col) = kreg[set][c];
+        *reinterpret_cast<uint4*>(sv + row * VP + col) =
+            ok ? vreg[set][c] : make_uint4(0, 0, 0, 0);
+      }
+      if (threadIdx.x < 2) {
+        const int pgq = ph[set][threadIdx.x];
+        s_pok[buf][threadIdx.x] = pgq >= 0 && pgq < P.phys_pages;
+      }
+    };
+    if (ntile > 1) {
+      page_ids(1, ph[1]);
+      load_shared(1, 1);
+    }
+    store_tile(0, 0);
+    __syncthreads();
+    auto step = [&](int i, int set) {  // set = i & 1, a compile-time constant
+      if (i >= ntile) return;
+      if (i + 2 < ntile) {
+        page_ids(i + 2, ph[set]);
+        load_shared(i + 2, set);
+      }
+      if (active)
+        compute(s_kv + set * BUF,
+                prefix_bits((tp0 + i) * kTile, pe, s_pok[set][0], s_pok[set][1]));
+      if (i + 1 < ntile) store_tile(i + 1, set ^ 1);
+      __syncthreads();
+    };
+    for (int i = 0; i < ntile; i += 2) {
+      step(i, 0);
+      step(i + 1, 1);
+    }
+  } else if (active) {
+    // ---- this wave alone: its request's tiles through its own LDS tile ----
+    const int pe = drafts ? 0 : min(pbeg + P.chunk_tokens, mylen);
+    const int ntile_p = pe > pbeg ? (pe - 1) / kTile - tp0 + 1 : 0;
+    const int ntile = ntile_p + (drafts ? (P.nodes + kTile - 1) / kTile : 0);
+    _Float16* sk = s_kv + wave * BUF;
+    _Float16* sv = sk + kTile * KP;
+    uint4 preg[CPL], qreg[CPL];  // K and V chunks of the next tile
+    bool vok[CPL];
+    int pg[2] = {pg_own[0], pg_own[1]};
+    auto load_tile = [&](int i) {
+      const bool is_draft = i >= ntile_p;
+      const int tbase = is_draft ? (i - ntile_p) * kTile : (tp0 + i) * kTile;
+      if (!is_draft && i > 0) {
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+          const int pi = (tp0 + i) * (kTile / BC_PAGE_SIZE) + q;
+          pg[q] = pi < P.max_pages ? P.pages[(size_t)b * P.max_pages + pi] : -1;
+        }
+      }
+#pragma unroll
+      for (int c = 0; c < CPL; ++c) {
+        const int chunk = lane + 64 * c;
+        const int row = chunk / CPR, col = 8 * (chunk % CPR);
+        if (!is_draft) {
+          const int pgq = pg[row / BC_PAGE_SIZE];
+          const int t = tbase + row;
+          const size_t off = prefix_off(pgq, row, col);
+          preg[c] = ldg16(P.k + off);
+          qreg[c] = ldg16(P.v + off);
+          vok[c] = pgq >= 0 && pgq < P.phys_pages && t >= pbeg && t < pe;
+        } else {
+          const int dn = tbase + row;
+          const size_t off =
+              (((size_t)b * P.nodes + min(dn, P.nodes - 1)) * P.hkv + kvh) * D + col;
+          preg[c] = ldg16(P.dk + off);
+          qreg[c] = ldg16(P.dv + off);
+          vok[c] = dn < P.nodes;
+        }
+      }
+    };
+    if (ntile > 0) load_tile(0);
+    for (int i = 0; i < ntile; ++i) {
+      const bool is_draft = i >= ntile_p;
+      const int tbase = is_draft ? (i - ntile_p) * kTile : (tp0 + i) * kTile;
+      const bool pok0 = pg[0] >= 0 && pg[0] < P.phys_pages;
+      const bool pok1 = pg[1] >= 0 && pg[1] < P.phys_pages;
+#pragma unroll
+      for (int c = 0; c < CPL; ++c) {
+        const int chunk = lane + 64 * c;
+        const int row = chunk / CPR, col = 8 * (chunk % CPR);
+        *reinterpret_cast<uint4*>(sk + row * KP + col) = preg[c];
+        *reinterpret_cast<uint4*>(sv + row * VP + col) = vok[c] ? qreg[c] : make_uint4(0, 0, 0, 0);
+      }
+      if (i + 1 < ntile) load_tile(i + 1);
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      compute(sk, is_draft ? draft_bits(tbase) : prefix_bits(tbase, pe, pok0, pok1));
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+  }
+  // This wave's rows: nothing to write when its request has no tokens in
+  // this prefix chunk (the merge does not read that slot).
+  const int own_end = drafts ? 0 : min(pbeg + P.chunk_tokens, mylen);
+  if (!rvalid || (!drafts && own_end <= pbeg)) return;
+  l += shfl_xor_f(l, 32);
+
+  if (drafts && mylen == 0) {
+    float* dst = P.out + (((size_t)b * P.nodes + node) * P.hq + h) * D;
+    const float inv = 1.f / l;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int jq = 0; jq < 4; ++jq)
+        *reinterpret_cast<float4*>(dst + 32 * dt + 8 * jq + 4 * g) =
+            make_float4(acc[dt][4 * jq] * inv, acc[dt][4 * jq + 1] * inv,
+                        acc[dt][4 * jq + 2] * inv, acc[dt][4 * jq + 3] * inv);
+  } else {
+    const size_t slot = slot_index(P, b, node, h, drafts ? P.prefix_parts : part);
+    float* dst = P.part_acc + slot * D;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int jq = 0; jq < 4; ++jq)
+        *reinterpret_cast<float4*>(dst + 32 * dt + 8 * jq + 4 * g) =
+            make_float4(acc[dt][4 * jq], acc[dt][4 * jq + 1], acc[dt][4 * jq + 2],
+                        acc[dt][4 * jq + 3]);
+    if (g == 0) {
+      P.part_ml[2 * slot] = m;
+      P.part_ml[2 * slot + 1] = l;
+    }
+  }
+}
+
 // Combines the prefix chunks and the draft part of every (b, node, h): one
 // wave per output row, lane p reads slot p's (max, sum), the weights are
 // formed once and every lane accumulates its dims with independent loads.
@@ -881,48 +1252,82 @@ int row_units(int row_tiles, bool rows_kernel) {
   return rows_kernel ? (row_tiles + kWaves - 1) / kWaves : row_tiles;
 }
 
-void tree_chunking(const bc_shape& s, int nodes, int* chunk_tokens, int* parts) {
-  const int group = s.query_heads / s.kv_heads;
-  const int row_tiles = (nodes * group + 31) / 32;
-  const int cus = bch::device_cus();
-  const bool rows = rows_kernel_for(s.batch, s.kv_heads, row_tiles, true, cus);
-  const long long units = (long long)s.batch * s.kv_heads * row_units(row_tiles, rows);
-  const int max_tokens = s.max_pages * BC_PAGE_SIZE;
-  // tree_rows_kernel walks its tiles in series, so it takes two workgroups
-  // per CU (two fit); tree_kernel's four waves split the tiles, one per CU.
-  long long want = (rows ? 2LL * cus : cus) / units - 1;
-  // With units in (cus/3, cus/2] the rule above gives tree_kernel a single
-  // chunk, which leaves half or more of the CUs idle while each workgroup
-  // walks the whole prefix; two chunks plus the draft part keep every
-  // workgroup resident (two per CU) and measured 25-26 us against 35 us at
-  // 12 and 16 requests of a 2048-token prefix.  More units than that
-  // measured slower with two.
-  if (!rows && want < 2 && 2LL * units <= cus) want = 2;
+// bc_tree_verify_shared_ws runs tree_group_kernel for one row tile per
+// (request, KV head) and at least two full groups of four requests; at four
+// requests or fewer it measured slower than tree_kernel even on one shared
+// prefix (4 x 2048: 15.2 against 14.6 us).
+bool group_kernel_for(int batch, int row_tiles) {
+  return row_tiles == 1 && batch >= 2 * kWaves;
+}
+
+// Prefix tokens per chunk for `want` chunks: multiples of 32, at least 128,
+// and at most 63 chunks (the merge reads one partial per lane).
+int chunk_for(int max_tokens, long long want) {
   if (want < 1) want = 1;
   int chunk = (int)((max_tokens + want - 1) / want);
   chunk = (chunk + kTile - 1) / kTile * kTile;
   if (chunk < 128) chunk = 128;
-  // The merge reads one partial per lane: at most 63 prefix chunks.
   const int min_chunk = (max_tokens + 62) / 63;
   if (chunk < min_chunk) chunk = (min_chunk + kTile - 1) / kTile * kTile;
+  return chunk;
+}
+
+void tree_chunking(const bc_shape& s, int nodes, bool grouped, int* chunk_tokens,
+                   int* parts) {
+  const int group = s.query_heads / s.kv_heads;
+  const int row_tiles = (nodes * group + 31) / 32;
+  const int cus = bch::device_cus();
+  const int max_tokens = s.max_pages * BC_PAGE_SIZE;
+  int chunk;
+  if (grouped) {
+    // tree_group_kernel walks its tiles in series: two workgroups per CU,
+    // unless the 128-token floor leaves a partial second round, which then
+    // shrinks to one round (8 x 2053 tokens: 288 workgroups 18.4 us, 224
+    // workgroups 17.7 us).
+    const long long units = (long long)s.kv_heads * ((s.batch + kWaves - 1) / kWaves);
+    chunk = chunk_for(max_tokens, 2LL * cus / units - 1);
+    const long long wgs = ((max_tokens + chunk - 1) / chunk + 1) * units;
+    if (wgs > cus && wgs < 2LL * cus - units) chunk = chunk_for(max_tokens, cus / units - 1);
+  } else {
+    const bool rows = rows_kernel_for(s.batch, s.kv_heads, row_tiles, true, cus);
+    const long long units = (long long)s.batch * s.kv_heads * row_units(row_tiles, rows);
+    // tree_rows_kernel walks its tiles in series, so it takes two workgroups
+    // per CU (two fit); tree_kernel's four waves split the tiles, one per CU.
+    long long want = (rows ? 2LL * cus : cus) / units - 1;
+    // With units in (cus/3, cus/2] the rule above gives tree_kernel a single
+    // chunk, which leaves half or more of the CUs idle while each workgroup
+    // walks the whole prefix; two chunks plus the draft part keep every
+    // workgroup resident (two per CU) and measured 25-26 us against 35 us at
+    // 12 and 16 requests of a 2048-token prefix.  More units than that
+    // measured slower with two.
+    if (!rows && want < 2 && 2LL * units <= cus) want = 2;
+    chunk = chunk_for(max_tokens, want);
+  }
   *chunk_tokens = chunk;
   *parts = (max_tokens + chunk - 1) / chunk;
 }
 
-size_t tree_workspace(const bc_shape& s, int nodes, int* chunk_tokens, int* parts) {
-  tree_chunking(s, nodes, chunk_tokens, parts);
+size_t tree_workspace(const bc_shape& s, int nodes, bool grouped, int* chunk_tokens,
+                      int* parts) {
+  tree_chunking(s, nodes, grouped, chunk_tokens, parts);
   if (*parts <= 1) return 0;
   const size_t slots = (size_t)s.batch * nodes * s.query_heads * (*parts + 1);
   const size_t acc = (slots * s.dim * sizeof(float) + 255) & ~(size_t)255;
   return acc + slots * 2 * sizeof(float);
 }
 
-hipError_t launch_tree(TreeParams& P, int dim, int parts, hipStream_t st) {
+hipError_t launch_tree(TreeParams& P, int dim, int parts, bool grouped, hipStream_t st) {
   const bool rows_kernel = rows_kernel_for(P.batch, P.hkv, P.row_tiles, P.part_acc != nullptr,
                                            bch::device_cus());
+  const bool group_kernel = grouped && P.part_acc;
   const dim3 grid(
-      (unsigned)((size_t)parts * P.batch * P.hkv * row_units(P.row_tiles, rows_kernel)));
-  if (rows_kernel) {
+      group_kernel
+          ? (unsigned)((size_t)parts * P.hkv * ((P.batch + kWaves - 1) / kWaves))
+          : (unsigned)((size_t)parts * P.batch * P.hkv * row_units(P.row_tiles, rows_kernel)));
+  if (group_kernel) {
+    if (dim == 64) tree_group_kernel<64><<<grid, kThreads, 0, st>>>(P);
+    else tree_group_kernel<128><<<grid, kThreads, 0, st>>>(P);
+  } else if (rows_kernel) {
     if (dim == 64) tree_rows_kernel<64><<<grid, kThreads, 0, st>>>(P);
     else tree_rows_kernel<128><<<grid, kThreads, 0, st>>>(P);
   } else {
@@ -952,25 +1357,28 @@ extern "C" int bc_tree_verify(bc_shape s, bc_tree_inputs in, int nodes,
     return BC_ERROR_INVALID_VALUE;
   TreeParams P = make_params(s, in, nodes);
   P.prefix_parts = 0;
-  return launch_tree(P, s.dim, 1, reinterpret_cast<hipStream_t>(stream));
+  return launch_tree(P, s.dim, 1, false, reinterpret_cast<hipStream_t>(stream));
 }
 
-extern "C" size_t bc_tree_verify_workspace_size(bc_shape s, int nodes) {
-  if (s.batch < 1 || s.query_heads < 1 || s.kv_heads < 1 ||
-      s.query_heads % s.kv_heads || (s.dim != 64 && s.dim != 128) ||
-      s.max_pages < 1 || nodes < 1 || nodes > BC_MAX_TREE_NODES)
-    return 0;
-  int chunk = 0, parts = 0;
-  return tree_workspace(s, nodes, &chunk, &parts);
+namespace {
+
+bool tree_shape_ok(const bc_shape& s, int nodes) {
+  return s.batch >= 1 && s.query_heads >= 1 && s.kv_heads >= 1 &&
+         s.query_heads % s.kv_heads == 0 && (s.dim == 64 || s.dim == 128) &&
+         s.max_pages >= 1 && nodes >= 1 && nodes <= BC_MAX_TREE_NODES;
 }
 
-extern "C" int bc_tree_verify_ws(bc_shape s, bc_tree_inputs in, int nodes,
-                                 void* workspace, size_t workspace_bytes,
-                                 bc_stream_t stream) {
+bool grouped_for(const bc_shape& s, int nodes) {
+  const int row_tiles = (nodes * (s.query_heads / s.kv_heads) + 31) / 32;
+  return group_kernel_for(s.batch, row_tiles);
+}
+
+int tree_ws_call(bc_shape s, bc_tree_inputs in, int nodes, bool grouped, void* workspace,
+                 size_t workspace_bytes, bc_stream_t stream) {
   if (!tree_args_ok(s, in, nodes) || !tree_ptrs_aligned(in))
     return BC_ERROR_INVALID_VALUE;
   int chunk = 0, parts = 0;
-  const size_t need = tree_workspace(s, nodes, &chunk, &parts);
+  const size_t need = tree_workspace(s, nodes, grouped, &chunk, &parts);
   if (!workspace || need == 0 || workspace_bytes < need || !aligned16(workspace))
     return bc_tree_verify(s, in, nodes, stream);
   TreeParams P = make_params(s, in, nodes);
@@ -980,5 +1388,33 @@ extern "C" int bc_tree_verify_ws(bc_shape s, bc_tree_inputs in, int nodes,
   const size_t acc = (slots * s.dim * sizeof(float) + 255) & ~(size_t)255;
   P.part_acc = static_cast<float*>(workspace);
   P.part_ml = reinterpret_cast<float*>(static_cast<char*>(workspace) + acc);
-  return launch_tree(P, s.dim, parts + 1, reinterpret_cast<hipStream_t>(stream));
+  return launch_tree(P, s.dim, parts + 1, grouped, reinterpret_cast<hipStream_t>(stream));
+}
+
+}  // namespace
+
+extern "C" size_t bc_tree_verify_workspace_size(bc_shape s, int nodes) {
+  if (!tree_shape_ok(s, nodes)) return 0;
+  int chunk = 0, parts = 0;
+  return tree_workspace(s, nodes, false, &chunk, &parts);
+}
+
+extern "C" int bc_tree_verify_ws(bc_shape s, bc_tree_inputs in, int nodes,
+                                 void* workspace, size_t workspace_bytes,
+                                 bc_stream_t stream) {
+  return tree_ws_call(s, in, nodes, false, workspace, workspace_bytes, stream);
+}
+
+extern "C" size_t bc_tree_verify_shared_workspace_size(bc_shape s, int nodes) {
+  if (!tree_shape_ok(s, nodes)) return 0;
+  int chunk = 0, parts = 0;
+  return tree_workspace(s, nodes, grouped_for(s, nodes), &chunk, &parts);
+}
+
+extern "C" int bc_tree_verify_shared_ws(bc_shape s, bc_tree_inputs in, int nodes,
+                                        void* workspace, size_t workspace_bytes,
+                                        bc_stream_t stream) {
+  if (!tree_shape_ok(s, nodes)) return BC_ERROR_INVALID_VALUE;
+  return tree_ws_call(s, in, nodes, grouped_for(s, nodes), workspace, workspace_bytes,
+                      stream);
 }

@@ -48,6 +48,17 @@ inline hipError_t tree_verify(Shape shape, TreeInputs in, int nodes, void* works
       bc_tree_verify_ws(shape, in, nodes, workspace, workspace_bytes, to_bc(stream)));
 }
 
+// Requests forked from one prefix: see bc_tree_verify_shared_ws.
+inline size_t tree_verify_shared_workspace_size(Shape shape, int nodes) {
+  return bc_tree_verify_shared_workspace_size(shape, nodes);
+}
+
+inline hipError_t tree_verify_shared(Shape shape, TreeInputs in, int nodes, void* workspace,
+                                     size_t workspace_bytes, hipStream_t stream = nullptr) {
+  return static_cast<hipError_t>(bc_tree_verify_shared_ws(shape, in, nodes, workspace,
+                                                          workspace_bytes, to_bc(stream)));
+}
+
 inline hipError_t commit_path(Shape shape, const half_bits* draft_k,
                               const half_bits* draft_v, half_bits* cache_k,
                               half_bits* cache_v, const int* path_nodes,

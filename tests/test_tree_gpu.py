@@ -19,11 +19,12 @@ pytestmark = pytest.mark.gpu
 
 
 def _check(fix, oracle, atol=3e-4, what=""):
+    """bc_tree_verify, bc_tree_verify_ws and bc_tree_verify_shared_ws."""
     k, v, pages, lengths, dq, dk, dv, par = fix
     expected = oracle.tree(k, v, pages, lengths, dq, dk, dv, par, threads=16)
-    for ws in (False, True):
-        out = G.tree(k, v, pages, lengths, dq, dk, dv, par, workspace=ws)
-        G.gate(out, expected, atol, f"{what} workspace={ws}")
+    for ws, shared in ((False, False), (True, False), (True, True)):
+        out = G.tree(k, v, pages, lengths, dq, dk, dv, par, workspace=ws, shared=shared)
+        G.gate(out, expected, atol, f"{what} workspace={ws} shared={shared}")
     return expected
 
 
@@ -159,25 +160,31 @@ def _group_fixture(rng, lengths, share, nodes=7, hq=32, hkv=8, d=128, cow_last=(
 @pytest.mark.parametrize("case", [
     # every request on its own pages
     dict(lengths=[611, 95, 870, 402, 333, 777, 128, 640], share=[-1] * 8),
-    # requests 1-3 share request 0's pages, request 3 ending early; 5 and 6
-    # share request 4's, request 5 with a copied last page
-    dict(lengths=[613, 613, 613, 400, 613, 613, 613], share=[-1, 0, 0, 0, -1, 4, 4],
-         cow_last=(5,)),
-    # five requests on one page table
-    dict(lengths=[300] * 5, share=[-1, 0, 0, 0, 0]),
-    # an empty request beside three sharing ones (its drafts give the output)
-    dict(lengths=[300, 0, 300, 300], share=[-1, 0, 0, 0]),
+    # requests 1-3 share request 0's pages, request 3 ending early; 5-7
+    # share request 4's, request 5 with a copied last page; 8 and 9 share
+    # request 0's, 10 has its own (a last group of three)
+    dict(lengths=[613, 613, 613, 400, 613, 613, 613, 613, 613, 613, 250],
+         share=[-1, 0, 0, 0, -1, 4, 4, 4, 0, 0, -1], cow_last=(5,)),
+    # nine requests on one page table (a last group of one)
+    dict(lengths=[300] * 9, share=[-1] + [0] * 8),
+    # empty requests beside sharing ones (their drafts give the output)
+    dict(lengths=[300, 0, 300, 300, 300, 300, 0, 300], share=[-1] + [0] * 7),
     # page tables far longer than every request (empty prefix chunks)
-    dict(lengths=[100, 100, 100], share=[-1, 0, 0], extra_pages=38),
-    # two requests; D = 64, group 4, eight nodes (32 rows)
-    dict(lengths=[517, 517], share=[-1, 0], nodes=8, hq=8, hkv=2, d=64),
+    dict(lengths=[100] * 8, share=[-1] + [0] * 7, extra_pages=38),
+    # D = 64, group 4, eight nodes (32 rows)
+    dict(lengths=[517] * 8, share=[-1] + [0] * 7, nodes=8, hq=8, hkv=2, d=64),
     # group 1: 32 nodes fill the row tile and the draft tile
-    dict(lengths=[290, 290, 290, 290], share=[-1, 0, 0, 0], nodes=32, hq=8, hkv=8),
+    dict(lengths=[290] * 8, share=[-1] + [0] * 7, nodes=32, hq=8, hkv=8),
+    # fewer than eight requests: bc_tree_verify_shared_ws runs as bc_tree_verify_ws
+    dict(lengths=[613, 613, 400, 613, 613], share=[-1, 0, 0, -1, 3]),
 ])
 def test_per_request_page_tables(case, oracle):
     """Requests whose page tables share some pages and not others, end at
     different lengths, hold a copied last page or are empty, with and
-    without a workspace."""
+    without a workspace.  With eight or more requests of one row tile,
+    bc_tree_verify_shared_ws runs tree_group_kernel: four requests per
+    workgroup, each prefix chunk loaded once for all of them where their
+    page ids and chunk ends agree, else every wave on its own pages."""
     rng = np.random.default_rng(len(case["lengths"]) * 7 + sum(case["lengths"]))
     fix = _group_fixture(rng, **case)
     k, v, pages, lengths, dq, dk, dv, par = fix
