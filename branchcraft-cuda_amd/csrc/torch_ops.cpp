@@ -41,11 +41,13 @@ bc_half* hptr_mut(at::Tensor& t) {
   return reinterpret_cast<bc_half*>(t.data_ptr<at::Half>());
 }
 
-// Reference: tree_verify_cuda, bindings/torch_ops.cpp:22-67.
-at::Tensor tree_verify_hip(const at::Tensor& q, const at::Tensor& prefix_k,
-                           const at::Tensor& prefix_v, const at::Tensor& pages,
-                           const at::Tensor& lengths, const at::Tensor& draft_k,
-                           const at::Tensor& draft_v, const at::Tensor& parent) {
+// Reference: tree_verify_cuda, bindings/torch_ops.cpp:22-67.  `shared`
+// selects bc_tree_verify_shared_ws (requests forked from one prefix; no
+// reference counterpart) with the same checks and output.
+at::Tensor tree_verify_impl(const at::Tensor& q, const at::Tensor& prefix_k,
+                            const at::Tensor& prefix_v, const at::Tensor& pages,
+                            const at::Tensor& lengths, const at::Tensor& draft_k,
+                            const at::Tensor& draft_v, const at::Tensor& parent, bool shared) {
   check_dev_contig(q, "q", at::kHalf);
   check_dev_contig(prefix_k, "prefix_k", at::kHalf);
   check_dev_contig(prefix_v, "prefix_v", at::kHalf);
@@ -86,15 +88,34 @@ at::Tensor tree_verify_hip(const at::Tensor& q, const at::Tensor& prefix_k,
                    lengths.data_ptr<int>(), nullptr};
   bc_tree_inputs in{prefix, hptr(q), hptr(draft_k), hptr(draft_v),
                     parent.data_ptr<int>(), output.data_ptr<float>()};
-  const size_t ws_bytes = bc_tree_verify_workspace_size(shape, int(nodes));
+  const size_t ws_bytes = shared ? bc_tree_verify_shared_workspace_size(shape, int(nodes))
+                                 : bc_tree_verify_workspace_size(shape, int(nodes));
   at::Tensor ws;
   if (ws_bytes > 0)
     ws = at::empty({int64_t(ws_bytes)}, q.options().dtype(at::kByte));
-  check_launch(bc_tree_verify_ws(shape, in, int(nodes),
-                                 ws_bytes ? ws.data_ptr() : nullptr, ws_bytes,
-                                 current_stream()),
-               "tree_verify");
+  void* const wsp = ws_bytes ? ws.data_ptr() : nullptr;
+  check_launch(shared ? bc_tree_verify_shared_ws(shape, in, int(nodes), wsp, ws_bytes,
+                                                 current_stream())
+                      : bc_tree_verify_ws(shape, in, int(nodes), wsp, ws_bytes,
+                                          current_stream()),
+               shared ? "tree_verify_shared" : "tree_verify");
   return output;
+}
+
+at::Tensor tree_verify_hip(const at::Tensor& q, const at::Tensor& prefix_k,
+                           const at::Tensor& prefix_v, const at::Tensor& pages,
+                           const at::Tensor& lengths, const at::Tensor& draft_k,
+                           const at::Tensor& draft_v, const at::Tensor& parent) {
+  return tree_verify_impl(q, prefix_k, prefix_v, pages, lengths, draft_k, draft_v, parent,
+                          false);
+}
+
+at::Tensor tree_verify_shared_hip(const at::Tensor& q, const at::Tensor& prefix_k,
+                                  const at::Tensor& prefix_v, const at::Tensor& pages,
+                                  const at::Tensor& lengths, const at::Tensor& draft_k,
+                                  const at::Tensor& draft_v, const at::Tensor& parent) {
+  return tree_verify_impl(q, prefix_k, prefix_v, pages, lengths, draft_k, draft_v, parent,
+                          true);
 }
 
 // Reference: packed_decode_out_cuda, bindings/torch_ops.cpp:69-104.
@@ -273,6 +294,7 @@ TORCH_LIBRARY(branchcraft, m) {
   m.def("commit_path_(Tensor(a!) cache_k, Tensor(b!) cache_v, Tensor draft_k, Tensor draft_v, Tensor path_nodes, Tensor dest_pages, Tensor dest_slots, int request) -> ()");
   m.def("copy_pages_(Tensor(a!) cache_k, Tensor(b!) cache_v, Tensor src_pages, Tensor dst_pages) -> ()");
   m.def("commit_paths_(Tensor(a!) cache_k, Tensor(b!) cache_v, Tensor draft_k, Tensor draft_v, Tensor requests, Tensor path_nodes, Tensor dest_pages, Tensor dest_slots) -> ()");
+  m.def("tree_verify_shared(Tensor q, Tensor prefix_k, Tensor prefix_v, Tensor pages, Tensor lengths, Tensor draft_k, Tensor draft_v, Tensor parent) -> Tensor");
 }
 
 TORCH_LIBRARY_IMPL(branchcraft, CUDA, m) {
@@ -281,4 +303,5 @@ TORCH_LIBRARY_IMPL(branchcraft, CUDA, m) {
   m.impl("commit_path_", commit_path_hip);
   m.impl("copy_pages_", copy_pages_hip);
   m.impl("commit_paths_", commit_paths_hip);
+  m.impl("tree_verify_shared", tree_verify_shared_hip);
 }

@@ -28,6 +28,11 @@ def _fake_tree_verify(q, prefix_k, prefix_v, pages, lengths, draft_k, draft_v, p
     return q.new_empty(q.shape, dtype=torch.float32)
 
 
+@torch.library.register_fake("branchcraft::tree_verify_shared")
+def _fake_tree_verify_shared(q, prefix_k, prefix_v, pages, lengths, draft_k, draft_v, parent):
+    return q.new_empty(q.shape, dtype=torch.float32)
+
+
 @torch.library.register_fake("branchcraft::packed_decode_out")
 def _fake_packed_decode_out(q, packed_kv, pages, lengths, output, scale):
     return output
@@ -54,6 +59,14 @@ def tree_verify(q, prefix_k, prefix_v, pages, lengths, draft_k, draft_v, parent)
     """FP32 [batch, node, query head, dim] outputs; every node attends to its
     request's paged prefix and its own ancestor chain (itself included)."""
     return torch.ops.branchcraft.tree_verify(
+        q, prefix_k, prefix_v, pages, lengths, draft_k, draft_v, parent)
+
+
+def tree_verify_shared(q, prefix_k, prefix_v, pages, lengths, draft_k, draft_v, parent):
+    """tree_verify for requests forked from one prefix (no reference
+    counterpart): the same outputs, faster when the requests' page tables
+    agree and slower when they do not."""
+    return torch.ops.branchcraft.tree_verify_shared(
         q, prefix_k, prefix_v, pages, lengths, draft_k, draft_v, parent)
 
 
@@ -86,5 +99,5 @@ def commit_paths_(cache_k, cache_v, draft_k, draft_v, requests, path_nodes, dest
         cache_k, cache_v, draft_k, draft_v, requests, path_nodes, dest_pages, dest_slots)
 
 
-__all__ = ["tree_verify", "packed_decode_out", "commit_path_", "copy_pages_", "commit_paths_",
+__all__ = ["tree_verify", "tree_verify_shared", "packed_decode_out", "commit_path_", "copy_pages_", "commit_paths_",
            "LIBRARY_PATH"]

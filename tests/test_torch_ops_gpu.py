@@ -3,6 +3,7 @@
 
 * tree_verify: ancestor mask against the oracle (D=64/128, lengths [23, 0]),
   torch.compile(inductor) equality and opcheck schema/FakeTensor checks;
+* tree_verify_shared (added): forked requests against the oracle and tree_verify;
 * packed_decode_out: HND and NHD-transposed caches and the 5-D
   [P, 2, 16, Hkv, D] layout, output aliasing, and HIP-graph capture replayed
   several times with eager work in between, every replay checked;
@@ -50,6 +51,34 @@ def test_tree_mask_compile_and_opcheck(dim):
     compiled = torch.compile(bc.tree_verify, backend="inductor")
     torch.testing.assert_close(compiled(*args), actual)
     torch.library.opcheck(torch.ops.branchcraft.tree_verify, args,
+                          test_utils=("test_schema", "test_faketensor"))
+
+
+def test_tree_verify_shared_op_on_forked_requests():
+    """tree_verify_shared (bc_tree_verify_shared_ws): ten requests forked
+    from one page table, one with a copied last page and one shorter, match
+    the oracle and tree_verify; schema and FakeTensor checks as above."""
+    torch.manual_seed(8)
+    batch, nodes, hq, hkv, dim = 10, 7, 8, 2, 128
+    q = torch.randn(batch, nodes, hq, dim, device="cuda", dtype=torch.float16)
+    prefix_k = torch.randn(40, 16, hkv, dim, device="cuda", dtype=torch.float16)
+    prefix_v = torch.randn_like(prefix_k)
+    row = torch.randperm(38, device="cuda").to(torch.int32)[:30]
+    pages = row.repeat(batch, 1)
+    pages[3, 29] = 38  # a copy-on-write clone of the last page
+    lengths = torch.full((batch,), 470, device="cuda", dtype=torch.int32)
+    lengths[6] = 301
+    draft_k = torch.randn(batch, nodes, hkv, dim, device="cuda", dtype=torch.float16)
+    draft_v = torch.randn_like(draft_k)
+    parent = torch.tensor([[-1, 0, 0, 1, 1, 2, 2]] * batch, device="cuda", dtype=torch.int32)
+    args = (q, prefix_k, prefix_v, pages, lengths, draft_k, draft_v, parent)
+    actual = bc.tree_verify_shared(*args)
+    assert actual.dtype == torch.float32 and actual.shape == q.shape
+    qn, pk, pv, pg, ln, dk, dv, par = (a.cpu().numpy() for a in args)
+    expected = oracle_c.tree(pk, pv, pg, ln, qn, dk, dv, par, threads=8)
+    G.gate(actual.cpu().numpy(), expected, 3e-4, "tree_verify_shared op")
+    torch.testing.assert_close(actual, bc.tree_verify(*args), atol=2e-6, rtol=0)
+    torch.library.opcheck(torch.ops.branchcraft.tree_verify_shared, args,
                           test_utils=("test_schema", "test_faketensor"))
 
 
