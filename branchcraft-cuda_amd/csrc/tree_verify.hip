@@ -755,10 +755,10 @@ __global__ __launch_bounds__(kThreads, 2) void tree_rows_kernel(TreeParams P) {
 // one prefix chunk.  When the requests' page ids over the chunk and their
 // chunk ends agree -- requests forked from one prefix -- the workgroup loads
 // each 32-token tile once into LDS for all four (the tree_rows_kernel
-// pipeline: two 16-byte chunks of K and of V per thread, two tiles ahead,
+// pipeline: D/64 16-byte chunks of K and of V per thread, two tiles ahead,
 // one barrier per tile), so a CU reads the shared prefix once per four
 // requests instead of once per request.  Otherwise, and for the draft part,
-// every wave walks its own request's tiles with its own loads (eight chunks
+// every wave walks its own request's tiles with its own loads (D/16 chunks
 // of K and of V per lane, one tile ahead) through its own LDS tile.  Masks,
 // softmax and the P.V product are those of tree_kernel.
 template <int D>
