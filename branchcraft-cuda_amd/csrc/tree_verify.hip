@@ -1260,13 +1260,13 @@ bool group_kernel_for(int batch, int row_tiles) {
   return row_tiles == 1 && batch >= 2 * kWaves;
 }
 
-// Prefix tokens per chunk for `want` chunks: multiples of 32, at least 128,
-// and at most 63 chunks (the merge reads one partial per lane).
-int chunk_for(int max_tokens, long long want) {
+// Prefix tokens per chunk for `want` chunks: multiples of 32, at least
+// `floor`, and at most 63 chunks (the merge reads one partial per lane).
+int chunk_for(int max_tokens, long long want, int floor = 128) {
   if (want < 1) want = 1;
   int chunk = (int)((max_tokens + want - 1) / want);
   chunk = (chunk + kTile - 1) / kTile * kTile;
-  if (chunk < 128) chunk = 128;
+  if (chunk < floor) chunk = floor;
   const int min_chunk = (max_tokens + 62) / 63;
   if (chunk < min_chunk) chunk = (min_chunk + kTile - 1) / kTile * kTile;
   return chunk;
@@ -1281,13 +1281,15 @@ void tree_chunking(const bc_shape& s, int nodes, bool grouped, int* chunk_tokens
   int chunk;
   if (grouped) {
     // tree_group_kernel walks its tiles in series: two workgroups per CU,
-    // unless the 128-token floor leaves a partial second round, which then
+    // unless the chunk floor leaves a partial second round, which then
     // shrinks to one round (8 x 2053 tokens: 288 workgroups 18.4 us, 224
-    // workgroups 17.7 us).
+    // workgroups 17.7 us).  Its floor is three tiles (8 x 1024 tokens: 14.3
+    // against 14.9 us with four).
     const long long units = (long long)s.kv_heads * ((s.batch + kWaves - 1) / kWaves);
-    chunk = chunk_for(max_tokens, 2LL * cus / units - 1);
+    chunk = chunk_for(max_tokens, 2LL * cus / units - 1, 96);
     const long long wgs = ((max_tokens + chunk - 1) / chunk + 1) * units;
-    if (wgs > cus && wgs < 2LL * cus - units) chunk = chunk_for(max_tokens, cus / units - 1);
+    if (wgs > cus && wgs < 2LL * cus - units)
+      chunk = chunk_for(max_tokens, cus / units - 1, 96);
   } else {
     const bool rows = rows_kernel_for(s.batch, s.kv_heads, row_tiles, true, cus);
     const long long units = (long long)s.batch * s.kv_heads * row_units(row_tiles, rows);
