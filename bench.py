@@ -525,13 +525,19 @@ def bench_commit(cx, f):
 
 def cpu_baseline(c5_host):
     """C oracle on the whole config-5 workload: one thread (the reference's
-    oracle is single-threaded) and all host cores (capped at 16)."""
+    oracle is single-threaded), 16 threads (a one-GPU box's CPU share) and
+    every core this process may run on (os.sched_getaffinity), which gives
+    `value`; os.cpu_count() is reported beside it."""
     sys.path.insert(0, str(ROOT))
     from oracle import oracle_c
     q, cache, pages, lengths, strides, nbytes = c5_host
-    cores = min(16, os.cpu_count() or 1)
+    host_cpus = os.cpu_count() or 1
+    try:
+        cores = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        cores = host_cpus
     res = {}
-    for threads in (1, cores):
+    for threads in sorted({1, min(16, cores), cores}):
         reps = 1 if threads == 1 else 3
         times = []
         for _ in range(reps):
@@ -545,8 +551,11 @@ def cpu_baseline(c5_host):
         "kind": "port",
         "sample": ("whole config-5 workload (64 sequences, "
                    f"{int(lengths.sum())} tokens) through oracle/bc_oracle.c, "
-                   f"median of 3 at {cores} threads"),
+                   f"median of 3 at {cores} threads (every core in this process's "
+                   "affinity mask)"),
+        "host_cpu_count": host_cpus,
         "single_thread_gbs": round(nbytes / res[1] / 1e9, 3),
+        "sixteen_thread_gbs": round(nbytes / res[min(16, cores)] / 1e9, 3),
         "single_thread_s": round(res[1], 3), "multi_thread_s": round(res[cores], 3),
     }
 

@@ -104,4 +104,29 @@ __device__ __forceinline__ uint4 ldg16_stream(const uint16_t* p) {
   return make_uint4(w.x, w.y, w.z, w.w);
 }
 
+// Eight consecutive FP16 values; VEC selects one 16-byte load, otherwise
+// eight 2-byte loads (for tensors or strides that are not 16-byte aligned).
+// STREAM marks the 16-byte load non-temporal (data read once per call).
+template <bool VEC, bool STREAM = false>
+__device__ __forceinline__ uint4 load8(const uint16_t* p) {
+  if (VEC) return STREAM ? ldg16_stream(p) : ldg16(p);
+  uint32_t w[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) w[i] = (uint32_t)p[2 * i] | ((uint32_t)p[2 * i + 1] << 16);
+  return make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+// Four consecutive floats: one 16-byte store when VEC, else four stores.
+template <bool VEC>
+__device__ __forceinline__ void store4f(float* p, float a, float b, float c, float d) {
+  if (VEC) {
+    *reinterpret_cast<float4*>(p) = make_float4(a, b, c, d);
+  } else {
+    p[0] = a;
+    p[1] = b;
+    p[2] = c;
+    p[3] = d;
+  }
+}
+
 }  // namespace bcd

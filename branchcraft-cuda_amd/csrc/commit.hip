@@ -5,20 +5,23 @@
 // or torch copy_ (python/branchcraft_torch/transaction.py:133-134).
 // bc_commit_paths commits the accepted paths of several requests in one
 // launch; bc_copy_pages clones any number of pages in one launch.
-// Both are bit copies of FP16 rows moved as 16-byte vectors; every index is
-// range-checked on the device and an out-of-range entry is skipped rather
-// than written out of bounds.
+// Both are bit copies of FP16 rows, moved as 16-byte vectors when every
+// tensor pointer is 16-byte aligned and as single halves otherwise (the
+// reference accepts any `half*`); every index is range-checked on the device
+// and an out-of-range entry is skipped rather than written out of bounds.
 #include "bc_device.h"
 
 namespace {
 
 constexpr int kThreads = 256;
 
-// One workgroup per accepted node; K and V rows of Hkv*D halves each.  The
+// One workgroup per accepted node; K and V rows of Hkv*D halves each, moved
+// as `row_vec` elements of type E (uint4: eight halves, uint16_t: one).  The
 // node's request is `requests[i]` when a list is given, else `request`.
+template <typename E>
 __global__ __launch_bounds__(kThreads) void commit_kernel(
-    const uint4* __restrict__ draft_k, const uint4* __restrict__ draft_v,
-    uint4* __restrict__ cache_k, uint4* __restrict__ cache_v,
+    const E* __restrict__ draft_k, const E* __restrict__ draft_v,
+    E* __restrict__ cache_k, E* __restrict__ cache_v,
     const int32_t* __restrict__ requests, const int32_t* __restrict__ path_nodes,
     const int32_t* __restrict__ dest_pages,
     const int32_t* __restrict__ dest_slots, int request, int batch, int nodes,
@@ -39,9 +42,11 @@ __global__ __launch_bounds__(kThreads) void commit_kernel(
   }
 }
 
-// grid = (count, slices): workgroup (i, s) copies slice s of page pair i.
+// grid = (count, slices): workgroup (i, s) copies slice s of page pair i,
+// in elements of type E as for commit_kernel.
+template <typename E>
 __global__ __launch_bounds__(kThreads) void copy_pages_kernel(
-    uint4* __restrict__ cache_k, uint4* __restrict__ cache_v,
+    E* __restrict__ cache_k, E* __restrict__ cache_v,
     const int32_t* __restrict__ src_pages, const int32_t* __restrict__ dst_pages,
     int phys_pages, int page_vec, int slice_vec) {
   const int i = blockIdx.x;
@@ -62,6 +67,27 @@ bool aligned16(const void* p) {
   return (reinterpret_cast<uintptr_t>(p) & 15) == 0;
 }
 
+// Launches commit_kernel over `count` entries with 16-byte elements when all
+// four tensors allow it, single halves otherwise.
+hipError_t launch_commit(const bc_shape& s, const bc_half* draft_k, const bc_half* draft_v,
+                         bc_half* cache_k, bc_half* cache_v, const int32_t* requests,
+                         const int32_t* path_nodes, const int32_t* dest_pages,
+                         const int32_t* dest_slots, int request, int nodes, int count,
+                         hipStream_t st) {
+  const int row = s.kv_heads * s.dim;  // halves per K (or V) row
+  if (aligned16(draft_k) && aligned16(draft_v) && aligned16(cache_k) && aligned16(cache_v))
+    commit_kernel<uint4><<<dim3(count), kThreads, 0, st>>>(
+        reinterpret_cast<const uint4*>(draft_k), reinterpret_cast<const uint4*>(draft_v),
+        reinterpret_cast<uint4*>(cache_k), reinterpret_cast<uint4*>(cache_v), requests,
+        path_nodes, dest_pages, dest_slots, request, s.batch, nodes, s.physical_pages,
+        row / 8);
+  else
+    commit_kernel<uint16_t><<<dim3(count), kThreads, 0, st>>>(
+        draft_k, draft_v, cache_k, cache_v, requests, path_nodes, dest_pages, dest_slots,
+        request, s.batch, nodes, s.physical_pages, row);
+  return hipGetLastError();
+}
+
 }  // namespace
 
 extern "C" int bc_commit_path(bc_shape s, const bc_half* draft_k,
@@ -76,17 +102,9 @@ extern "C" int bc_commit_path(bc_shape s, const bc_half* draft_k,
       s.physical_pages < 1)
     return BC_ERROR_INVALID_VALUE;
   if (s.dim != 64 && s.dim != 128) return BC_ERROR_INVALID_VALUE;
-  if (!aligned16(draft_k) || !aligned16(draft_v) || !aligned16(cache_k) ||
-      !aligned16(cache_v))
-    return BC_ERROR_INVALID_VALUE;
-  const int row_vec = s.kv_heads * s.dim / 8;
-  commit_kernel<<<dim3(accepted), kThreads, 0,
-                  reinterpret_cast<hipStream_t>(stream)>>>(
-      reinterpret_cast<const uint4*>(draft_k),
-      reinterpret_cast<const uint4*>(draft_v), reinterpret_cast<uint4*>(cache_k),
-      reinterpret_cast<uint4*>(cache_v), nullptr, path_nodes, dest_pages, dest_slots,
-      request, s.batch, nodes, s.physical_pages, row_vec);
-  return hipGetLastError();
+  return launch_commit(s, draft_k, draft_v, cache_k, cache_v, nullptr, path_nodes,
+                       dest_pages, dest_slots, request, nodes, accepted,
+                       reinterpret_cast<hipStream_t>(stream));
 }
 
 extern "C" int bc_commit_paths(bc_shape s, const bc_half* draft_k,
@@ -100,16 +118,10 @@ extern "C" int bc_commit_paths(bc_shape s, const bc_half* draft_k,
       !dest_pages || !dest_slots || s.batch < 1 || nodes < 1 || count < 0 ||
       s.kv_heads < 1 || s.physical_pages < 1 || (s.dim != 64 && s.dim != 128))
     return BC_ERROR_INVALID_VALUE;
-  if (!aligned16(draft_k) || !aligned16(draft_v) || !aligned16(cache_k) ||
-      !aligned16(cache_v))
-    return BC_ERROR_INVALID_VALUE;
   if (count == 0) return BC_SUCCESS;
-  const int row_vec = s.kv_heads * s.dim / 8;
-  commit_kernel<<<dim3(count), kThreads, 0, reinterpret_cast<hipStream_t>(stream)>>>(
-      reinterpret_cast<const uint4*>(draft_k), reinterpret_cast<const uint4*>(draft_v),
-      reinterpret_cast<uint4*>(cache_k), reinterpret_cast<uint4*>(cache_v), requests,
-      path_nodes, dest_pages, dest_slots, 0, s.batch, nodes, s.physical_pages, row_vec);
-  return hipGetLastError();
+  return launch_commit(s, draft_k, draft_v, cache_k, cache_v, requests, path_nodes,
+                       dest_pages, dest_slots, 0, nodes, count,
+                       reinterpret_cast<hipStream_t>(stream));
 }
 
 extern "C" int bc_copy_pages(bc_shape s, bc_half* cache_k, bc_half* cache_v,
@@ -119,18 +131,24 @@ extern "C" int bc_copy_pages(bc_shape s, bc_half* cache_k, bc_half* cache_v,
   if (!cache_k || !cache_v || !src_pages || !dst_pages || count < 0 ||
       s.kv_heads < 1 || (s.dim != 64 && s.dim != 128) || s.physical_pages < 1)
     return BC_ERROR_INVALID_VALUE;
-  if (!aligned16(cache_k) || !aligned16(cache_v)) return BC_ERROR_INVALID_VALUE;
   if (count == 0) return BC_SUCCESS;
-  const int page_vec = BC_PAGE_SIZE * s.kv_heads * s.dim / 8;
-  const int slice_vec = 4 * kThreads;  // 16 KiB of K and of V per workgroup
-  const int slices = (page_vec + slice_vec - 1) / slice_vec;
-  copy_pages_kernel<<<dim3(count, slices), kThreads, 0,
-                      reinterpret_cast<hipStream_t>(stream)>>>(
-      reinterpret_cast<uint4*>(cache_k), reinterpret_cast<uint4*>(cache_v),
-      src_pages, dst_pages, s.physical_pages, page_vec, slice_vec);
+  const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const int page = BC_PAGE_SIZE * s.kv_heads * s.dim;  // halves per page of K (or V)
+  if (aligned16(cache_k) && aligned16(cache_v)) {
+    const int page_vec = page / 8;
+    const int slice_vec = 4 * kThreads;  // 16 KiB of K and of V per workgroup
+    const int slices = (page_vec + slice_vec - 1) / slice_vec;
+    copy_pages_kernel<uint4><<<dim3(count, slices), kThreads, 0, st>>>(
+        reinterpret_cast<uint4*>(cache_k), reinterpret_cast<uint4*>(cache_v), src_pages,
+        dst_pages, s.physical_pages, page_vec, slice_vec);
+  } else {
+    const int slice = 16 * kThreads;  // 8 KiB of K and of V per workgroup
+    copy_pages_kernel<uint16_t><<<dim3(count, (page + slice - 1) / slice), kThreads, 0, st>>>(
+        cache_k, cache_v, src_pages, dst_pages, s.physical_pages, page, slice);
+  }
   return hipGetLastError();
 }
 
 extern "C" const char* bc_version(void) {
-  return "branchcraft-mi355x 0.1 (gfx950)";
+  return "branchcraft-mi355x 0.2 (gfx950)";
 }

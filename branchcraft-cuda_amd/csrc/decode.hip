@@ -175,18 +175,6 @@ __device__ __forceinline__ void store_out(void* out, size_t idx, float x) {
   static_cast<OutT*>(out)[idx] = (OutT)x;
 }
 
-// Eight consecutive FP16 values; VEC selects one 16-byte load, otherwise
-// eight 2-byte loads (for strides or bases that are not 8-element aligned).
-// STREAM marks the 16-byte load non-temporal (K/V pages are read once).
-template <bool VEC, bool STREAM = false>
-__device__ __forceinline__ uint4 load8(const uint16_t* p) {
-  if (VEC) return STREAM ? ldg16_stream(p) : ldg16(p);
-  uint32_t w[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) w[i] = (uint32_t)p[2 * i] | ((uint32_t)p[2 * i + 1] << 16);
-  return make_uint4(w[0], w[1], w[2], w[3]);
-}
-
 __device__ __forceinline__ f16x4 lds_read_tr(const _Float16* p) {
   const i16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
       (__attribute__((address_space(3))) i16x4*)(p));
@@ -748,6 +736,9 @@ extern "C" int bc_auto_splits(bc_shape s, int max_length, int cu_count) {
   // measured faster at 512 sequences of up to 1024 tokens.
   if (s.batch < 1 || s.kv_heads < 1 || s.query_heads < 1 || s.query_heads % s.kv_heads)
     return 1;
+  // Contexts below 512 tokens never split (src/paged_gqa.cu:135): a merge
+  // launch costs more than the few pages a split would spread.
+  if (max_length < 512) return 1;
   const int cus = cu_count > 0 ? cu_count : 256;
   const int group = s.query_heads / s.kv_heads;
   const long long zdim = (long long)s.kv_heads * ((group + kHeadCols - 1) / kHeadCols);

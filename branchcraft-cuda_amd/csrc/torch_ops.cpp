@@ -13,6 +13,9 @@
 #include <c10/hip/HIPStream.h>
 #include <torch/library.h>
 
+#include <algorithm>
+#include <atomic>
+
 #include "branchcraft.h"
 
 namespace {
@@ -116,6 +119,74 @@ at::Tensor tree_verify_shared_hip(const at::Tensor& q, const at::Tensor& prefix_
                                   const at::Tensor& draft_v, const at::Tensor& parent) {
   return tree_verify_impl(q, prefix_k, prefix_v, pages, lengths, draft_k, draft_v, parent,
                           true);
+}
+
+// Compute units of a device, cached (an immutable attribute).
+int device_cus(int device) {
+  static std::atomic<int> cache[64];
+  if (device >= 0 && device < 64) {
+    const int v = cache[device].load(std::memory_order_relaxed);
+    if (v > 0) return v;
+  }
+  int n = 0;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess ||
+      n < 1)
+    n = 256;
+  if (device >= 0 && device < 64) cache[device].store(n, std::memory_order_relaxed);
+  return n;
+}
+
+// Paged GQA decode with FP32 output.  The reference exposes it only as the
+// C++ branchcraft::decode / auto_splits (include/branchcraft.hpp:39-41,
+// src/paged_gqa.cu:122-142); this op takes the same tensors as Inputs
+// (q [B,Hq,D], k/v [P,16,Hkv,D] FP16, pages [B,max_pages] and lengths [B]
+// int32).  splits == 0 picks the split count from the shape alone:
+// bc_auto_splits with the page table's capacity (max_pages * 16 tokens) as
+// the context bound, so the op never reads lengths back to the host and
+// can be captured in a HIP graph.  The split scratch comes from the caching
+// allocator on the current stream.
+at::Tensor paged_decode_hip(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v,
+                            const at::Tensor& pages, const at::Tensor& lengths,
+                            int64_t splits) {
+  check_dev_contig(q, "q", at::kHalf);
+  check_dev_contig(k, "k", at::kHalf);
+  check_dev_contig(v, "v", at::kHalf);
+  check_dev_contig(pages, "pages", at::kInt);
+  check_dev_contig(lengths, "lengths", at::kInt);
+  TORCH_CHECK(q.dim() == 3 && k.dim() == 4 && pages.dim() == 2 && lengths.dim() == 1,
+              "invalid paged decode tensor rank");
+  const int64_t b = q.size(0), hq = q.size(1), d = q.size(2), hkv = k.size(2);
+  TORCH_CHECK(b > 0 && hq > 0 && hkv > 0 && hq % hkv == 0 && (d == 64 || d == 128),
+              "unsupported paged decode shape");
+  TORCH_CHECK(k.size(0) > 0 && k.size(1) == BC_PAGE_SIZE && k.size(3) == d &&
+                  v.sizes() == k.sizes(),
+              "K/V cache shape mismatch");
+  TORCH_CHECK(pages.size(0) == b && pages.size(1) >= 1 && lengths.size(0) == b,
+              "paged decode metadata mismatch");
+  TORCH_CHECK(splits >= 0 && splits <= BC_MAX_SPLITS, "splits must be in [0, ",
+              BC_MAX_SPLITS, "]");
+  TORCH_CHECK(q.device() == k.device() && q.device() == v.device() &&
+                  q.device() == pages.device() && q.device() == lengths.device(),
+              "all tensors must share a device");
+  const c10::DeviceGuard guard(q.device());
+  bc_shape shape{int(b), int(hq), int(hkv), int(d), int(pages.size(1)), int(k.size(0))};
+  if (splits == 0) {
+    const int64_t cap = std::min<int64_t>(pages.size(1) * BC_PAGE_SIZE, 1 << 30);
+    splits = bc_auto_splits(shape, int(cap), device_cus(q.device().index()));
+  }
+  auto output = at::empty(q.sizes(), q.options().dtype(at::kFloat));
+  at::Tensor scratch;
+  bc_scratch scr{nullptr, nullptr};
+  if (splits > 1) {
+    const int64_t rows = splits * b * hq;
+    scratch = at::empty({rows * (d + 2)}, q.options().dtype(at::kFloat));
+    scr.partial_a = scratch.data_ptr<float>();
+    scr.partial_ml = scr.partial_a + rows * d;
+  }
+  bc_inputs in{hptr(q), hptr(k), hptr(v), pages.data_ptr<int>(), lengths.data_ptr<int>(),
+               output.data_ptr<float>()};
+  check_launch(bc_decode(shape, in, scr, int(splits), current_stream()), "paged_decode");
+  return output;
 }
 
 // Reference: packed_decode_out_cuda, bindings/torch_ops.cpp:69-104.
@@ -295,6 +366,7 @@ TORCH_LIBRARY(branchcraft, m) {
   m.def("copy_pages_(Tensor(a!) cache_k, Tensor(b!) cache_v, Tensor src_pages, Tensor dst_pages) -> ()");
   m.def("commit_paths_(Tensor(a!) cache_k, Tensor(b!) cache_v, Tensor draft_k, Tensor draft_v, Tensor requests, Tensor path_nodes, Tensor dest_pages, Tensor dest_slots) -> ()");
   m.def("tree_verify_shared(Tensor q, Tensor prefix_k, Tensor prefix_v, Tensor pages, Tensor lengths, Tensor draft_k, Tensor draft_v, Tensor parent) -> Tensor");
+  m.def("paged_decode(Tensor q, Tensor k, Tensor v, Tensor pages, Tensor lengths, int splits=0) -> Tensor");
 }
 
 TORCH_LIBRARY_IMPL(branchcraft, CUDA, m) {
@@ -304,4 +376,5 @@ TORCH_LIBRARY_IMPL(branchcraft, CUDA, m) {
   m.impl("copy_pages_", copy_pages_hip);
   m.impl("commit_paths_", commit_paths_hip);
   m.impl("tree_verify_shared", tree_verify_shared_hip);
+  m.impl("paged_decode", paged_decode_hip);
 }

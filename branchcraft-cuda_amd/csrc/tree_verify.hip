@@ -92,7 +92,7 @@ __device__ __forceinline__ size_t slot_index(const TreeParams& P, int b,
   return (((size_t)b * P.nodes + node) * P.hq + h) * (P.prefix_parts + 1) + part;
 }
 
-template <int D>
+template <int D, bool VEC>
 __global__ __launch_bounds__(kThreads, 2) void tree_kernel(TreeParams P) {
   constexpr int KS = D / 16;  // MFMA k-steps over the head dimension
   constexpr int DT = D / 32;  // 32-row output tiles over the head dimension
@@ -167,7 +167,7 @@ __global__ __launch_bounds__(kThreads, 2) void tree_kernel(TreeParams P) {
   {
     const uint16_t* qp = P.dq + (((size_t)b * P.nodes + node) * P.hq + h) * D + 8 * g;
 #pragma unroll
-    for (int j = 0; j < QS; ++j) qf[j] = ldg16(qp + 16 * (wave * QS + j));
+    for (int j = 0; j < QS; ++j) qf[j] = load8<VEC>(qp + 16 * (wave * QS + j));
   }
 
   _Float16* vs = reinterpret_cast<_Float16*>(s_mem) + wave * kTile * VP;
@@ -226,7 +226,7 @@ __global__ __launch_bounds__(kThreads, 2) void tree_kernel(TreeParams P) {
       vp = P.dv + off;
     }
 #pragma unroll
-    for (int s = 0; s < KS; ++s) kr[s] = ldg16(kp + 16 * s + 8 * g);
+    for (int s = 0; s < KS; ++s) kr[s] = load8<VEC>(kp + 16 * s + 8 * g);
   };
 
   auto process = [&](int idx, const uint4 (&kr)[KS], const uint16_t* vp, bool tv,
@@ -234,7 +234,7 @@ __global__ __launch_bounds__(kThreads, 2) void tree_kernel(TreeParams P) {
     if (idx >= nmine) return;  // padding step
     uint4 vr[KS];
 #pragma unroll
-    for (int s = 0; s < KS; ++s) vr[s] = ldg16(vp + 16 * s + 8 * g);
+    for (int s = 0; s < KS; ++s) vr[s] = load8<VEC>(vp + 16 * s + 8 * g);
     const int it = wave + kWaves * idx;
     const bool is_draft = it >= ntile_p;
     const int tbase = is_draft ? (it - ntile_p) * kTile : (tp0 + it) * kTile;
@@ -439,9 +439,9 @@ __global__ __launch_bounds__(kThreads, 2) void tree_kernel(TreeParams P) {
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
       for (int jq = 0; jq < 4; ++jq)
-        *reinterpret_cast<float4*>(dst + 32 * dt + 8 * jq + 4 * g) =
-            make_float4(acc[dt][4 * jq] * inv, acc[dt][4 * jq + 1] * inv,
-                        acc[dt][4 * jq + 2] * inv, acc[dt][4 * jq + 3] * inv);
+        store4f<VEC>(dst + 32 * dt + 8 * jq + 4 * g, acc[dt][4 * jq] * inv,
+                     acc[dt][4 * jq + 1] * inv, acc[dt][4 * jq + 2] * inv,
+                     acc[dt][4 * jq + 3] * inv);
   } else {
     const int p = drafts ? P.prefix_parts : part;
     const size_t slot = slot_index(P, b, node, h, p);
@@ -468,7 +468,7 @@ __global__ __launch_bounds__(kThreads, 2) void tree_kernel(TreeParams P) {
 // the A-operand layout and V through transpose reads, and owns its rows to
 // the end: no merge between waves.  Masks, softmax and the P.V product are
 // those of tree_kernel.
-template <int D>
+template <int D, bool VEC>
 __global__ __launch_bounds__(kThreads, 2) void tree_rows_kernel(TreeParams P) {
   constexpr int KS = D / 16;
   constexpr int DT = D / 32;
@@ -525,7 +525,7 @@ __global__ __launch_bounds__(kThreads, 2) void tree_rows_kernel(TreeParams P) {
   {
     const uint16_t* qp = P.dq + (((size_t)b * P.nodes + node) * P.hq + h) * D + 8 * g;
 #pragma unroll
-    for (int s = 0; s < KS; ++s) qB[s] = rvalid ? ldg16(qp + 16 * s) : make_uint4(0, 0, 0, 0);
+    for (int s = 0; s < KS; ++s) qB[s] = rvalid ? load8<VEC>(qp + 16 * s) : make_uint4(0, 0, 0, 0);
   }
   static_assert(BC_MAX_TREE_NODES <= kThreads, "one parent entry per thread");
   const bool has_parent = (int)threadIdx.x < P.nodes;
@@ -563,14 +563,14 @@ __global__ __launch_bounds__(kThreads, 2) void tree_rows_kernel(TreeParams P) {
         ok = pok && t >= pbeg && t < pend;
         off = (pok ? ((size_t)pgq * BC_PAGE_SIZE + row % BC_PAGE_SIZE) * tok_stride : 0) +
               (size_t)kvh * D + col;
-        kreg[set][c] = ldg16(P.k + off);
-        vreg[set][c] = ldg16(P.v + off);
+        kreg[set][c] = load8<VEC>(P.k + off);
+        vreg[set][c] = load8<VEC>(P.v + off);
       } else {
         const int dn = tbase + row;
         ok = dn < P.nodes;
         off = (((size_t)b * P.nodes + min(dn, P.nodes - 1)) * P.hkv + kvh) * D + col;
-        kreg[set][c] = ldg16(P.dk + off);
-        vreg[set][c] = ldg16(P.dv + off);
+        kreg[set][c] = load8<VEC>(P.dk + off);
+        vreg[set][c] = load8<VEC>(P.dv + off);
       }
       vok[set][c] = ok;
     }
@@ -729,9 +729,9 @@ __global__ __launch_bounds__(kThreads, 2) void tree_rows_kernel(TreeParams P) {
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
       for (int jq = 0; jq < 4; ++jq)
-        *reinterpret_cast<float4*>(dst + 32 * dt + 8 * jq + 4 * g) =
-            make_float4(acc[dt][4 * jq] * inv, acc[dt][4 * jq + 1] * inv,
-                        acc[dt][4 * jq + 2] * inv, acc[dt][4 * jq + 3] * inv);
+        store4f<VEC>(dst + 32 * dt + 8 * jq + 4 * g, acc[dt][4 * jq] * inv,
+                     acc[dt][4 * jq + 1] * inv, acc[dt][4 * jq + 2] * inv,
+                     acc[dt][4 * jq + 3] * inv);
   } else {
     const int p = drafts ? P.prefix_parts : part;
     const size_t slot = slot_index(P, b, node, h, p);
@@ -761,7 +761,7 @@ __global__ __launch_bounds__(kThreads, 2) void tree_rows_kernel(TreeParams P) {
 // every wave walks its own request's tiles with its own loads (D/16 chunks
 // of K and of V per lane, one tile ahead) through its own LDS tile.  Masks,
 // softmax and the P.V product are those of tree_kernel.
-template <int D>
+template <int D, bool VEC>
 __global__ __launch_bounds__(kThreads, 2) void tree_group_kernel(TreeParams P) {
   constexpr int KS = D / 16;
   constexpr int DT = D / 32;
@@ -843,7 +843,7 @@ __global__ __launch_bounds__(kThreads, 2) void tree_group_kernel(TreeParams P) {
   {
     const uint16_t* qp = P.dq + (((size_t)b * P.nodes + node) * P.hq + h) * D + 8 * g;
 #pragma unroll
-    for (int s = 0; s < KS; ++s) qB[s] = rvalid ? ldg16(qp + 16 * s) : make_uint4(0, 0, 0, 0);
+    for (int s = 0; s < KS; ++s) qB[s] = rvalid ? load8<VEC>(qp + 16 * s) : make_uint4(0, 0, 0, 0);
   }
   if (drafts && lane < 32)
     s_parent[wave][lane] = P.parent[(size_t)b * P.nodes + min(lane, P.nodes - 1)];
@@ -868,8 +868,8 @@ __global__ __launch_bounds__(kThreads, 2) void tree_group_kernel(TreeParams P) {
       const int chunk = (int)threadIdx.x + kThreads * c;
       const int row = chunk / CPR, col = 8 * (chunk % CPR);
       const size_t off = prefix_off(pg[row / BC_PAGE_SIZE], row, col);
-      kreg[set][c] = ldg16(P.k + off);
-      vreg[set][c] = ldg16(P.v + off);
+      kreg[set][c] = load8<VEC>(P.k + off);
+      vreg[set][c] = load8<VEC>(P.v + off);
     }
   };
   if (!drafts) load_shared(0, 0);
@@ -1049,15 +1049,15 @@ __global__ __launch_bounds__(kThreads, 2) void tree_group_kernel(TreeParams P) {
           const int pgq = pg[row / BC_PAGE_SIZE];
           const int t = tbase + row;
           const size_t off = prefix_off(pgq, row, col);
-          preg[c] = ldg16(P.k + off);
-          qreg[c] = ldg16(P.v + off);
+          preg[c] = load8<VEC>(P.k + off);
+          qreg[c] = load8<VEC>(P.v + off);
           vok[c] = pgq >= 0 && pgq < P.phys_pages && t >= pbeg && t < pe;
         } else {
           const int dn = tbase + row;
           const size_t off =
               (((size_t)b * P.nodes + min(dn, P.nodes - 1)) * P.hkv + kvh) * D + col;
-          preg[c] = ldg16(P.dk + off);
-          qreg[c] = ldg16(P.dv + off);
+          preg[c] = load8<VEC>(P.dk + off);
+          qreg[c] = load8<VEC>(P.dv + off);
           vok[c] = dn < P.nodes;
         }
       }
@@ -1098,9 +1098,9 @@ __global__ __launch_bounds__(kThreads, 2) void tree_group_kernel(TreeParams P) {
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
       for (int jq = 0; jq < 4; ++jq)
-        *reinterpret_cast<float4*>(dst + 32 * dt + 8 * jq + 4 * g) =
-            make_float4(acc[dt][4 * jq] * inv, acc[dt][4 * jq + 1] * inv,
-                        acc[dt][4 * jq + 2] * inv, acc[dt][4 * jq + 3] * inv);
+        store4f<VEC>(dst + 32 * dt + 8 * jq + 4 * g, acc[dt][4 * jq] * inv,
+                     acc[dt][4 * jq + 1] * inv, acc[dt][4 * jq + 2] * inv,
+                     acc[dt][4 * jq + 3] * inv);
   } else {
     const size_t slot = slot_index(P, b, node, h, drafts ? P.prefix_parts : part);
     float* dst = P.part_acc + slot * D;
@@ -1318,7 +1318,21 @@ size_t tree_workspace(const bc_shape& s, int nodes, bool grouped, int* chunk_tok
   return acc + slots * 2 * sizeof(float);
 }
 
-hipError_t launch_tree(TreeParams& P, int dim, int parts, bool grouped, hipStream_t st) {
+template <int D, bool VEC>
+void launch_tree_kernel(const TreeParams& P, bool group_kernel, bool rows_kernel, dim3 grid,
+                        hipStream_t st) {
+  if (group_kernel)
+    tree_group_kernel<D, VEC><<<grid, kThreads, 0, st>>>(P);
+  else if (rows_kernel)
+    tree_rows_kernel<D, VEC><<<grid, kThreads, 0, st>>>(P);
+  else
+    tree_kernel<D, VEC><<<grid, kThreads, 0, st>>>(P);
+}
+
+// vec: every FP16 tensor and the output are 16-byte aligned (16-byte loads
+// and stores); otherwise the kernels move single halves and floats.
+hipError_t launch_tree(TreeParams& P, int dim, int parts, bool grouped, bool vec,
+                       hipStream_t st) {
   const bool rows_kernel = rows_kernel_for(P.batch, P.hkv, P.row_tiles, P.part_acc != nullptr,
                                            bch::device_cus());
   const bool group_kernel = grouped && P.part_acc;
@@ -1326,15 +1340,12 @@ hipError_t launch_tree(TreeParams& P, int dim, int parts, bool grouped, hipStrea
       group_kernel
           ? (unsigned)((size_t)parts * P.hkv * ((P.batch + kWaves - 1) / kWaves))
           : (unsigned)((size_t)parts * P.batch * P.hkv * row_units(P.row_tiles, rows_kernel)));
-  if (group_kernel) {
-    if (dim == 64) tree_group_kernel<64><<<grid, kThreads, 0, st>>>(P);
-    else tree_group_kernel<128><<<grid, kThreads, 0, st>>>(P);
-  } else if (rows_kernel) {
-    if (dim == 64) tree_rows_kernel<64><<<grid, kThreads, 0, st>>>(P);
-    else tree_rows_kernel<128><<<grid, kThreads, 0, st>>>(P);
+  if (dim == 64) {
+    if (vec) launch_tree_kernel<64, true>(P, group_kernel, rows_kernel, grid, st);
+    else launch_tree_kernel<64, false>(P, group_kernel, rows_kernel, grid, st);
   } else {
-    if (dim == 64) tree_kernel<64><<<grid, kThreads, 0, st>>>(P);
-    else tree_kernel<128><<<grid, kThreads, 0, st>>>(P);
+    if (vec) launch_tree_kernel<128, true>(P, group_kernel, rows_kernel, grid, st);
+    else launch_tree_kernel<128, false>(P, group_kernel, rows_kernel, grid, st);
   }
   hipError_t err = hipGetLastError();
   if (err != hipSuccess || !P.part_acc) return err;
@@ -1355,11 +1366,11 @@ bool tree_ptrs_aligned(const bc_tree_inputs& in) {
 
 extern "C" int bc_tree_verify(bc_shape s, bc_tree_inputs in, int nodes,
                               bc_stream_t stream) {
-  if (!tree_args_ok(s, in, nodes) || !tree_ptrs_aligned(in))
-    return BC_ERROR_INVALID_VALUE;
+  if (!tree_args_ok(s, in, nodes)) return BC_ERROR_INVALID_VALUE;
   TreeParams P = make_params(s, in, nodes);
   P.prefix_parts = 0;
-  return launch_tree(P, s.dim, 1, false, reinterpret_cast<hipStream_t>(stream));
+  return launch_tree(P, s.dim, 1, false, tree_ptrs_aligned(in),
+                     reinterpret_cast<hipStream_t>(stream));
 }
 
 namespace {
@@ -1377,8 +1388,7 @@ bool grouped_for(const bc_shape& s, int nodes) {
 
 int tree_ws_call(bc_shape s, bc_tree_inputs in, int nodes, bool grouped, void* workspace,
                  size_t workspace_bytes, bc_stream_t stream) {
-  if (!tree_args_ok(s, in, nodes) || !tree_ptrs_aligned(in))
-    return BC_ERROR_INVALID_VALUE;
+  if (!tree_args_ok(s, in, nodes)) return BC_ERROR_INVALID_VALUE;
   int chunk = 0, parts = 0;
   const size_t need = tree_workspace(s, nodes, grouped, &chunk, &parts);
   if (!workspace || need == 0 || workspace_bytes < need || !aligned16(workspace))
@@ -1390,7 +1400,8 @@ int tree_ws_call(bc_shape s, bc_tree_inputs in, int nodes, bool grouped, void* w
   const size_t acc = (slots * s.dim * sizeof(float) + 255) & ~(size_t)255;
   P.part_acc = static_cast<float*>(workspace);
   P.part_ml = reinterpret_cast<float*>(static_cast<char*>(workspace) + acc);
-  return launch_tree(P, s.dim, parts + 1, grouped, reinterpret_cast<hipStream_t>(stream));
+  return launch_tree(P, s.dim, parts + 1, grouped, tree_ptrs_aligned(in),
+                     reinterpret_cast<hipStream_t>(stream));
 }
 
 }  // namespace

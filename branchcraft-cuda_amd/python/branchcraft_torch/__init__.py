@@ -3,7 +3,9 @@
 Importing this module loads ``_C.so`` (built in-tree by
 ``branchcraft-cuda_amd/build.py``) which registers ``torch.ops.branchcraft``
 with the reference's schemas (bindings/torch_ops.cpp:144-148 of
-Haaziq386/branchcraft-cuda) plus ``copy_pages_``.  There is no CPU or
+Haaziq386/branchcraft-cuda) plus ``paged_decode`` (the reference's C++
+``branchcraft::decode``), ``copy_pages_``, ``commit_paths_`` and
+``tree_verify_shared``.  There is no CPU or
 Python fallback: a missing extension raises ImportError, and the ops have
 only a GPU implementation.
 
@@ -36,6 +38,11 @@ def _fake_tree_verify_shared(q, prefix_k, prefix_v, pages, lengths, draft_k, dra
 @torch.library.register_fake("branchcraft::packed_decode_out")
 def _fake_packed_decode_out(q, packed_kv, pages, lengths, output, scale):
     return output
+
+
+@torch.library.register_fake("branchcraft::paged_decode")
+def _fake_paged_decode(q, k, v, pages, lengths, splits=0):
+    return q.new_empty(q.shape, dtype=torch.float32)
 
 
 @torch.library.register_fake("branchcraft::commit_path_")
@@ -79,6 +86,13 @@ def packed_decode_out(q, packed_kv, pages, lengths, output, scale):
         q, packed_kv, pages, lengths, output, scale)
 
 
+def paged_decode(q, k, v, pages, lengths, splits=0):
+    """Paged GQA decode (the reference's C++ ``branchcraft::decode``): FP32
+    [batch, query head, dim] output over K/V pages [P, 16, kv_heads, dim].
+    ``splits=0`` picks the split count from the shape (no host sync)."""
+    return torch.ops.branchcraft.paged_decode(q, k, v, pages, lengths, splits)
+
+
 def commit_path_(cache_k, cache_v, draft_k, draft_v, path_nodes, dest_pages,
                  dest_slots, request):
     """Write accepted draft K/V to preallocated physical destinations."""
@@ -87,7 +101,9 @@ def commit_path_(cache_k, cache_v, draft_k, draft_v, path_nodes, dest_pages,
 
 
 def copy_pages_(cache_k, cache_v, src_pages, dst_pages):
-    """Clone whole pages (K and V): cache[dst[i]] <- cache[src[i]]."""
+    """Clone whole pages (K and V): cache[dst[i]] <- cache[src[i]].  All
+    pairs copy at once: destinations must be distinct and none may also be
+    a source."""
     return torch.ops.branchcraft.copy_pages_(cache_k, cache_v, src_pages, dst_pages)
 
 
@@ -99,5 +115,5 @@ def commit_paths_(cache_k, cache_v, draft_k, draft_v, requests, path_nodes, dest
         cache_k, cache_v, draft_k, draft_v, requests, path_nodes, dest_pages, dest_slots)
 
 
-__all__ = ["tree_verify", "tree_verify_shared", "packed_decode_out", "commit_path_", "copy_pages_", "commit_paths_",
-           "LIBRARY_PATH"]
+__all__ = ["tree_verify", "tree_verify_shared", "packed_decode_out", "paged_decode",
+           "commit_path_", "copy_pages_", "commit_paths_", "LIBRARY_PATH"]

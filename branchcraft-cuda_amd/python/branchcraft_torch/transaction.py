@@ -146,6 +146,12 @@ class PagedTreeCache:
         if not plans:
             return
         cows = [p.cow for p in plans if p.cow is not None]
+        # copy_pages_ runs every pair at once: a destination must be fresh,
+        # so distinct and never another pair's source (the page owner only
+        # hands out free pages as clone targets).
+        dsts = [fresh for _, fresh in cows]
+        if len(set(dsts)) != len(dsts) or set(dsts) & {old for old, _ in cows}:
+            raise RuntimeError("copy-on-write clones overlap")
         rows = [(i, node, page, slot) for i, (p, path) in enumerate(zip(plans, paths))
                 for node, page, slot in zip(path, p.dest_pages, p.dest_slots)]
         flat = [x for c in cows for x in c] + [x for r in rows for x in r]

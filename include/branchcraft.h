@@ -88,23 +88,33 @@ typedef struct bc_tree_inputs {
  * splits > 1 spreads the batch's pages over equal ranges of the concatenated
  * sequences, at most (splits - 1) * B + 1 workgroups, and merges the FP32
  * partial softmax states of the sequences a range boundary cuts; the
- * partials fit the reference's scratch sizes.
+ * partials fit the reference's scratch sizes for `splits`.  FP16 tensors
+ * that are not 16-byte aligned are read with 2-byte loads.
  * Replaces branchcraft::decode, include/branchcraft.hpp:39-40
- * (src/paged_gqa.cu:198-208).  Rejects: batch/Hq/Hkv < 1, Hq % Hkv != 0,
+ * (src/paged_gqa.cu:122-132).  Rejects: batch/Hq/Hkv < 1, Hq % Hkv != 0,
  * dim not 64/128, max_pages or physical_pages < 1, splits outside
  * [1, BC_MAX_SPLITS], a null input, null scratch with splits > 1. */
 int bc_decode(bc_shape shape, bc_inputs in, bc_scratch scratch, int splits,
               bc_stream_t stream);
 
 /* Split-count heuristic for bc_decode on a device with `cu_count` compute
- * units.  Replaces branchcraft::auto_splits, include/branchcraft.hpp:41
- * (src/paged_gqa.cu:210-218); retuned for 256-CU MI355X workgroups. */
+ * units; returns a value in [1, BC_MAX_SPLITS], 1 for max_length < 512.
+ * Replaces branchcraft::auto_splits, include/branchcraft.hpp:41
+ * (src/paged_gqa.cu:134-142), retuned for 256-CU MI355X workgroups: unlike
+ * the reference (at most 16) it may return more than 16 (33 for 4
+ * sequences of 32K tokens, 128 for one), so the caller sizes bc_decode's
+ * scratch for the value it passes (splits*B*Hq*D and splits*B*Hq*2 floats).
+ * The C++ branchcraft::auto_splits caps the result at 16 by default. */
 int bc_auto_splits(bc_shape shape, int max_length, int cu_count);
 
 /* Ancestor-only tree verification over a paged prefix.
  * Replaces branchcraft::tree_verify, include/branchcraft.hpp:55-56
  * (src/tree_attention.cu:93-105).  Runs without scratch: one workgroup
- * per (request, KV head, row tile) streams the whole prefix. */
+ * per (request, KV head, row tile) streams the whole prefix.  Tensors that
+ * are not 16-byte aligned are read and written element by element.
+ * Rejects: batch/Hq/Hkv < 1, Hq % Hkv != 0, dim not 64/128, max_pages < 1,
+ * nodes outside [1, BC_MAX_TREE_NODES], a null K/V, page table, lengths,
+ * draft tensor, parent array or output. */
 int bc_tree_verify(bc_shape shape, bc_tree_inputs in, int nodes,
                    bc_stream_t stream);
 
@@ -141,7 +151,8 @@ int bc_tree_verify_shared_ws(bc_shape shape, bc_tree_inputs in, int nodes,
  * cache[dest_pages[i], dest_slots[i]] <- draft[request, path_nodes[i]] for
  * i < accepted, K and V, bit-exact.  Entries whose node, page or slot is out
  * of range are skipped.  shape.kv_heads, shape.dim, shape.batch and
- * shape.physical_pages describe the tensors.
+ * shape.physical_pages describe the tensors.  Any 2-byte aligned pointers
+ * work (16-byte copies when all four are 16-byte aligned).
  * Replaces branchcraft::commit_path, include/branchcraft.hpp:61-65
  * (src/tree_attention.cu:107-122). */
 int bc_commit_path(bc_shape shape, const bc_half* draft_k,
@@ -166,7 +177,10 @@ int bc_commit_paths(bc_shape shape, const bc_half* draft_k,
 
 /* Copy whole pages (all 16 slots, K and V) cache[dst_pages[i]] <-
  * cache[src_pages[i]] for i < count: the copy-on-write clone of a shared
- * partial page.  Out-of-range page ids are skipped.  No reference C++
+ * partial page.  Out-of-range page ids and src == dst are skipped.  All
+ * pairs copy concurrently, so the destinations must be distinct and no
+ * destination may also be a source; otherwise the result is unspecified.
+ * Any 2-byte aligned pointers work.  No reference C++
  * counterpart: it replaces the D2D copies at src/main.cu:276-281 and the
  * torch copy_ at python/branchcraft_torch/transaction.py:133-134. */
 int bc_copy_pages(bc_shape shape, bc_half* cache_k, bc_half* cache_v,
@@ -180,7 +194,7 @@ int bc_copy_pages(bc_shape shape, bc_half* cache_k, bc_half* cache_v,
  * contiguous.  kv_stride == dim gives the reference's logical
  * [P,Hkv,16,2D] layout; [P,2,16,Hkv,D] uses kv_stride = 16*Hkv*D.
  * Replaces branchcraft::packed_decode, include/branchcraft.hpp:70-74
- * (src/packed_decode.cu:188-206), adding kv_stride.  Rejects the bc_decode
+ * (src/packed_decode.cu:64-82), adding kv_stride.  Rejects the bc_decode
  * shape rules plus any stride < 1 and scale <= 0 (or NaN). */
 int bc_packed_decode(bc_shape shape, const bc_half* q, const bc_half* packed_kv,
                      const int32_t* pages, const int32_t* lengths,

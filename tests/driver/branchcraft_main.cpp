@@ -51,12 +51,19 @@ struct DeviceBuffer {
   ~DeviceBuffer() {
     if (ptr) (void)hipFree(ptr);
   }
-  void upload(const std::vector<T>& v) {
+  void upload(const std::vector<T>& v) { upload<T>(v); }
+  // Host data of another element type with the same size: FP16 bit patterns
+  // (uint16_t) into `half` buffers.
+  template <typename U>
+  void upload(const std::vector<U>& v) {
+    static_assert(sizeof(U) == sizeof(T), "same element size");
     if (v.size() != count) throw std::runtime_error("upload size mismatch");
     CHECK(hipMemcpy(ptr, v.data(), count * sizeof(T), hipMemcpyHostToDevice));
   }
-  std::vector<T> download() const {
-    std::vector<T> v(count);
+  template <typename U = T>
+  std::vector<U> download() const {
+    static_assert(sizeof(U) == sizeof(T), "same element size");
+    std::vector<U> v(count);
     CHECK(hipMemcpy(v.data(), ptr, count * sizeof(T), hipMemcpyDeviceToHost));
     return v;
   }
@@ -137,12 +144,12 @@ float max_abs_error(const std::vector<float>& a, const std::vector<float>& b) {
 }
 
 struct GpuFixture {
-  DeviceBuffer<h16> q, k, v;
+  DeviceBuffer<half> q, k, v;
   DeviceBuffer<int> pages, lengths;
   DeviceBuffer<float> output, partial_a, partial_ml;
   Shape shape;
   int max_splits;
-  explicit GpuFixture(const Fixture& f, int max_splits = 256)
+  explicit GpuFixture(const Fixture& f, int max_splits = BC_MAX_SPLITS)
       : q(f.q.size()), k(f.k.size()), v(f.v.size()), pages(f.pages.size()),
         lengths(f.lengths.size()),
         output((size_t)f.shape.batch * f.shape.query_heads * f.shape.dim),
@@ -221,7 +228,7 @@ std::vector<float> cpu_tree(const TreeFixture& t, int threads = 1) {
 
 struct TreeGpu {
   GpuFixture prefix;
-  DeviceBuffer<h16> draft_q, draft_k, draft_v;
+  DeviceBuffer<half> draft_q, draft_k, draft_v;
   DeviceBuffer<int> parent;
   DeviceBuffer<float> output;
   DeviceBuffer<char> workspace;
@@ -281,17 +288,22 @@ int cu_count() {
   return n;
 }
 
-std::string device_name() {
-  hipDeviceProp_t prop{};
-  CHECK(hipGetDeviceProperties(&prop, 0));
-  return prop.name;
-}
-
 std::string device_arch() {
   hipDeviceProp_t prop{};
   CHECK(hipGetDeviceProperties(&prop, 0));
   std::string a = prop.gcnArchName;
   return a.substr(0, a.find(':'));
+}
+
+// The marketing name when the runtime reports one; some boxes leave
+// hipDeviceProp_t::name blank, and the CSV's gpu column then names the
+// architecture instead.
+std::string device_name() {
+  hipDeviceProp_t prop{};
+  CHECK(hipGetDeviceProperties(&prop, 0));
+  std::string n = prop.name;
+  while (!n.empty() && (n.back() == ' ' || n.back() == '\n')) n.pop_back();
+  return n.empty() ? "AMD " + device_arch() : n;
 }
 
 int runtime_version() {
@@ -381,7 +393,7 @@ void run_tree_tests() {
   const int pn[3] = {0, 1, 3}, pg[3] = {new_page, new_page, new_page}, sl[3] = {1, 2, 3};
   oracle_commit(2, t.nodes, 8, 128, t.prefix.shape.physical_pages, t.draft_k.data(),
                 t.draft_v.data(), ek.data(), ev.data(), pn, pg, sl, 0, 3);
-  if (gpu.prefix.k.download() != ek || gpu.prefix.v.download() != ev)
+  if (gpu.prefix.k.download<h16>() != ek || gpu.prefix.v.download<h16>() != ev)
     throw std::runtime_error("commit pages differ from the oracle");
   auto committed_pages = t.prefix.pages;
   auto committed_lengths = t.prefix.lengths;
@@ -430,7 +442,7 @@ void run_bench(const std::string& path, bool quick) {
       for (int i = 0; i < b; ++i) lengths[i] = context - (i % 4) * context / 8;
       Fixture f = make_fixture(b, 32, 8, 128, lengths, 17 + b + context);
       GpuFixture gpu(f);
-      const int splits = branchcraft::auto_splits(f.shape, context, cus);
+      const int splits = branchcraft::auto_splits(f.shape, context, cus, BC_MAX_SPLITS);
       gpu.run(1);
       const auto baseline = gpu.output.download();
       gpu.run(splits);
@@ -548,7 +560,7 @@ void report(const char* what, double us, double bytes, double cpu1, double cpun,
 }
 
 void run_config(int n) {
-  const int cores = std::max(1u, std::min(16u, std::thread::hardware_concurrency()));
+  const int cores = (int)std::max(1u, std::thread::hardware_concurrency());
   const int cus = cu_count();
   std::cout << "device " << device_name() << " (" << device_arch() << ", " << cus
             << " CUs); host threads " << std::thread::hardware_concurrency() << '\n';
@@ -563,7 +575,8 @@ void run_config(int n) {
       f = make_fixture(4, 32, 8, 128, lens, 4, 1.0f, 16);
     }
     GpuFixture gpu(f);
-    const int splits = branchcraft::auto_splits(f.shape, *std::max_element(f.lengths.begin(), f.lengths.end()), cus);
+    const int splits = branchcraft::auto_splits(
+        f.shape, *std::max_element(f.lengths.begin(), f.lengths.end()), cus, BC_MAX_SPLITS);
     std::vector<float> ref1, refn;
     const double c1 = cpu_seconds([&] { ref1 = cpu_decode(f, 1); });
     const double cn = cpu_seconds([&] { refn = cpu_decode(f, cores); });
@@ -587,8 +600,8 @@ void run_config(int n) {
     std::cout << "config " << n << " max_abs_error=" << err << '\n';
     report("tree_verify", us, bytes, c1, cn, cores);
     Fixture expanded = make_expanded_fixture(t);
-    GpuFixture flat(expanded, 256);
-    const int splits = branchcraft::auto_splits(expanded.shape, prefix + 7, cus);
+    GpuFixture flat(expanded);
+    const int splits = branchcraft::auto_splits(expanded.shape, prefix + 7, cus, BC_MAX_SPLITS);
     const double e1 = median_latency_us([&] { return flat.launch(1); });
     const double es = median_latency_us([&] { return flat.launch(splits); });
     std::cout << std::fixed << std::setprecision(3) << "expanded-prefix decode: " << e1
@@ -609,7 +622,7 @@ void run_config(int n) {
     std::vector<h16> cache((size_t)NB * 2 * 16 * hkv * d), q((size_t)B * hq * d);
     rng.fill(cache, 1.0f);
     rng.fill(q, 1.0f);
-    DeviceBuffer<h16> dcache(cache.size()), dq(q.size()), dout(q.size());
+    DeviceBuffer<half> dcache(cache.size()), dq(q.size()), dout(q.size());
     DeviceBuffer<int> dpages(pages.size()), dlens(lens.size());
     dcache.upload(cache);
     dq.upload(q);
@@ -634,7 +647,7 @@ void run_config(int n) {
     });
     CHECK(launch());
     CHECK(hipDeviceSynchronize());
-    const auto out16 = dout.download();
+    const auto out16 = dout.download<h16>();
     float err = 0;
     for (size_t i = 0; i < out16.size(); ++i)
       err = std::max(err, std::fabs(oracle_h2f(out16[i]) - ref1[i]));

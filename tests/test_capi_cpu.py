@@ -159,6 +159,9 @@ def test_auto_splits_policy():
     and keeps short contexts and larger batches unsplit."""
     lib = capi.load()
     assert lib.bc_auto_splits(_shape(batch=1), 63, 256) == 1  # tiny contexts stay whole
+    # below 512 tokens nothing splits, whatever the batch (src/paged_gqa.cu:135)
+    for batch in (1, 64, 512):
+        assert lib.bc_auto_splits(_shape(batch=batch), 511, 256) == 1
     # short contexts whose (sequence, head block) workgroups fit the CUs run
     # unsplit: eight waves share each sequence's pages, no merge kernel
     assert lib.bc_auto_splits(_shape(batch=1), 512, 256) == 1
@@ -189,7 +192,10 @@ def test_workspace_sizes():
     assert lib.bc_packed_decode_workspace_size(capi.Shape(4, 32, 8, 128, 8, 64)) == 0
     assert lib.bc_packed_decode_workspace_size(capi.Shape(4, 32, 8, 128, 64, 64)) == 0
     assert lib.bc_packed_decode_workspace_size(capi.Shape(4, 32, 8, 128, 65, 64)) > 0
-    assert lib.bc_packed_decode_workspace_size(capi.Shape(64, 32, 8, 128, 8, 64)) > 0
+    # Tables below 512 tokens never split; from 512 on, batches whose
+    # workgroups outnumber the CUs do.
+    assert lib.bc_packed_decode_workspace_size(capi.Shape(64, 32, 8, 128, 8, 64)) == 0
+    assert lib.bc_packed_decode_workspace_size(capi.Shape(64, 32, 8, 128, 32, 64)) > 0
     assert lib.bc_packed_decode_workspace_size(capi.Shape(4, 32, 8, 96, 80, 64)) == 0
     c3 = capi.Shape(8, 32, 8, 128, 129, 160)
     assert lib.bc_tree_verify_workspace_size(c3, 7) > 0
@@ -233,6 +239,10 @@ def test_torch_ops_register_reference_schemas():
     assert "commit_paths_(Tensor(a!) cache_k, Tensor(b!) cache_v" in str(
         torch.ops.branchcraft.commit_paths_.default._schema)
     assert "copy_pages_(Tensor(a!) cache_k" in str(torch.ops.branchcraft.copy_pages_.default._schema)
+    # the reference's C++ decode as an op
+    assert str(torch.ops.branchcraft.paged_decode.default._schema) == (
+        "branchcraft::paged_decode(Tensor q, Tensor k, Tensor v, Tensor pages, "
+        "Tensor lengths, int splits=0) -> Tensor")
 
 
 def test_ops_have_no_cpu_fallback():

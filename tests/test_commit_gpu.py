@@ -49,6 +49,41 @@ def test_random_commits_and_page_copies_bit_exact(oracle):
     assert np.array_equal(tv.cpu().numpy().view(np.uint16), ev.view(np.uint16))
 
 
+def _offset_copy(a: np.ndarray, elems: int) -> torch.Tensor:
+    """A GPU copy of `a` whose data pointer sits `elems` FP16 elements past a
+    16-byte boundary."""
+    buf = torch.empty(a.size + 16, device="cuda", dtype=torch.float16)
+    view = buf[elems:elems + a.size].view(a.shape)
+    view.copy_(torch.from_numpy(a))
+    assert view.data_ptr() % 16 != 0
+    return view
+
+
+@pytest.mark.parametrize("elems", [1, 3])
+def test_unaligned_commits_and_page_copies_bit_exact(elems, oracle):
+    """Cache and draft tensors 2 or 6 bytes off 16-byte alignment (the
+    reference accepts any `half*`): bc_copy_pages, bc_commit_path and
+    bc_commit_paths take their element-wise paths, bit-exact."""
+    rng = np.random.default_rng(22 + elems)
+    P, hkv, d, b, n = 12, 8, 64, 3, 7
+    ck = rng.standard_normal((P, 16, hkv, d)).astype(np.float16)
+    cv = rng.standard_normal((P, 16, hkv, d)).astype(np.float16)
+    dk = rng.standard_normal((b, n, hkv, d)).astype(np.float16)
+    dv = rng.standard_normal((b, n, hkv, d)).astype(np.float16)
+    tk, tv = _offset_copy(ck, elems), _offset_copy(cv, elems)
+    tdk, tdv = _offset_copy(dk, elems), _offset_copy(dv, elems)
+    G.copy_pages(tk, tv, [4, 9], [10, 11])
+    ek, ev = oracle.copy_pages(ck, cv, [4, 9], [10, 11])
+    path, dpg, dsl = [0, 3, 5, 6], [10, 10, 99, 11], [3, 4, 5, 15]
+    G.commit(tk, tv, tdk, tdv, path, dpg, dsl, 2)
+    ek, ev = oracle.commit(ek, ev, dk, dv, path, dpg, dsl, 2)
+    G.commit_paths(tk, tv, tdk, tdv, [0, 1], [2, 4], [3, 5], [0, 9])
+    for req, node, page, slot in ((0, 2, 3, 0), (1, 4, 5, 9)):
+        ek, ev = oracle.commit(ek, ev, dk, dv, [node], [page], [slot], req)
+    assert np.array_equal(tk.cpu().numpy().view(np.uint16), ek.view(np.uint16))
+    assert np.array_equal(tv.cpu().numpy().view(np.uint16), ev.view(np.uint16))
+
+
 def test_driver_commit_sibling_rollback(oracle):
     """src/main.cu:264-313: two requests share a 17-token prefix; clone the
     partial page to P-1, commit path {0,1,3} at slots {1,2,3}, and decode

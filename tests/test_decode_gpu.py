@@ -8,7 +8,9 @@ beyond the reference's cap, benchmark config 1 and config 4 at full size.
 
 import numpy as np
 import pytest
+import torch
 
+import branchcraft_capi as capi
 from oracle import oracle_np
 import gpu_helpers as G
 
@@ -56,7 +58,14 @@ def test_config4_split_k_long_context(oracle):
     q, k, v, pages, lengths = oracle_np.paged_fixture(rng, 4, 32, 8, 128, lens, spare=16,
                                                      sigma=1.0)
     expected = oracle.decode(q, k, v, pages, lengths, threads=16)
-    for splits in (16, 64):
+    # bc_auto_splits' own choice, which bench.py times (33 on 256 CUs), and
+    # the reference's cap of 16 that branchcraft::auto_splits returns.
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    shape = capi.Shape(4, 32, 8, 128, pages.shape[1], k.shape[0])
+    auto = G.lib().bc_auto_splits(shape, int(lens.max()), cus)
+    if cus == 256:
+        assert auto == 33
+    for splits in sorted({16, auto, 64}):
         out = G.decode(q, k, v, pages, lengths, splits)
         G.gate(out, expected, 2e-3, f"config4 splits={splits}")
         G.gate(out, expected, 3e-4, f"config4 splits={splits} (reference gate)")

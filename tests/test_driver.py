@@ -74,7 +74,7 @@ def test_driver_quick_benches_write_reference_csv(tmp_path):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("n", [1, 2, 3, 5])
+@pytest.mark.parametrize("n", [1, 2, 3, 4, 5])
 def test_driver_configs_pass_parity(n):
     r = run("config", str(n), timeout=600)
     print(r.stdout, r.stderr)

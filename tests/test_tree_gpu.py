@@ -206,3 +206,72 @@ def test_misaligned_workspace_runs_single_pass():
     plain = G.tree(*fix, workspace=False)
     shifted = G.tree(*fix, workspace=True, ws_offset=4)
     assert np.array_equal(plain, shifted)
+
+
+def test_malformed_parent_arrays_end_the_walk(oracle):
+    """Parent arrays that do not form a tree (the reference walks them
+    unbounded, src/tree_attention.cu:50-52): a 2-cycle, a self-loop, parents
+    >= N and below -1, a parent after its child, every node its own parent
+    and one cycle through all nodes.  Every kernel's walk is bounded by N
+    steps and stops outside [0, N), so each row attends to the set of nodes
+    its walk reaches, as the oracle's walk (which stops at the first repeat)
+    does; all three entry points run, the shared one on tree_group_kernel."""
+    rng = np.random.default_rng(61)
+    fix = list(oracle_np.tree_fixture(rng, 8, 300, 7, sigma=1.0, parents="random"))
+    par = fix[7].copy()
+    par[1] = [-1, 0, 3, 2, 1, 4, 5]      # nodes 2 <-> 3 form a cycle
+    par[2, 4] = 4                        # self-loop
+    par[3, 5], par[3, 6] = 7, 1000       # parents past the last node
+    par[4, 1], par[4, 5] = 5, 0          # a parent after its child
+    par[5] = np.arange(7)                # every node its own parent
+    par[6, 3] = -7                       # negative, not -1
+    par[7] = (np.arange(7) + 1) % 7      # one cycle through all nodes
+    fix[7] = par.astype(np.int32)
+    expected = _check(tuple(fix), oracle, what="malformed parents")
+    # the oracle's own sets: node 3 of request 1 sees {3, 2}; request 7 sees all
+    closed = oracle_np.tree(*fix)
+    G.gate(expected, closed, 1e-5, "oracle vs closed form")
+
+
+@pytest.mark.parametrize("offset", [2, 6])
+def test_unaligned_tensors(offset, oracle):
+    """FP16 tensors and the output shifted off 16-byte alignment (the
+    reference accepts any `half*`): every entry point takes its element-wise
+    path and matches the oracle."""
+    import torch
+
+    rng = np.random.default_rng(70 + offset)
+    fix = oracle_np.tree_fixture(rng, 2, 300, 7, parents="random")
+    k, v, pages, lengths, dq, dk, dv, par = fix
+    expected = oracle.tree(*fix)
+    b, n, hq, d = dq.shape
+
+    def shifted(a):
+        flat = torch.from_numpy(np.ascontiguousarray(a).reshape(-1)).cuda()
+        buf = torch.empty(flat.numel() + 16, device="cuda", dtype=flat.dtype)
+        view = buf[offset // flat.element_size():][:flat.numel()]
+        view.copy_(flat)
+        return view
+
+    tk, tv, tq, tdk, tdv = (shifted(a) for a in (k, v, dq, dk, dv))
+    assert tk.data_ptr() % 16 != 0
+    tp = torch.from_numpy(pages).cuda()
+    tl = torch.from_numpy(lengths).cuda()
+    tpar = torch.from_numpy(par).cuda()
+    obuf = torch.full((b * n * hq * d + 8,), float("nan"), device="cuda")
+    out = obuf[1:1 + b * n * hq * d]
+    shape = capi.Shape(b, hq, k.shape[2], d, pages.shape[1], k.shape[0])
+    prefix = capi.Inputs(None, tk.data_ptr(), tv.data_ptr(), tp.data_ptr(), tl.data_ptr(), None)
+    ins = capi.TreeInputs(prefix, tq.data_ptr(), tdk.data_ptr(), tdv.data_ptr(),
+                          tpar.data_ptr(), out.data_ptr())
+    L = G.lib()
+    nbytes = L.bc_tree_verify_workspace_size(shape, n)
+    ws = torch.empty(max(1, nbytes), device="cuda", dtype=torch.uint8)
+    stream = G.stream()
+    for name, call in (("bc_tree_verify", lambda: L.bc_tree_verify(shape, ins, n, stream)),
+                       ("bc_tree_verify_ws", lambda: L.bc_tree_verify_ws(
+                           shape, ins, n, ws.data_ptr(), nbytes, stream))):
+        out.fill_(float("nan"))
+        G.check(call(), name)
+        torch.cuda.synchronize()
+        G.gate(out.cpu().numpy().reshape(b, n, hq, d), expected, 3e-4, f"{name} offset={offset}")
