@@ -73,6 +73,9 @@ struct TreeParams {
   int chunk_tokens;         // prefix tokens per chunk (workspace mode)
   int prefix_parts;         // chunk slots per row; slot prefix_parts = drafts
   float scale_log2;
+  // tree_split_kernel: parts per unit and tiles per part; with parts > 1,
+  // part_acc/part_ml hold P.parts slots per output row.
+  int parts, tiles_per_part;
 };
 
 __device__ __forceinline__ f16x8 as_f16x8(const uint4 u) {
@@ -458,6 +461,421 @@ __global__ __launch_bounds__(kThreads, 2) void tree_kernel(TreeParams P) {
       P.part_ml[2 * slot + 1] = l;
     }
   }
+}
+
+// Split tree verification.  Unit = (request, KV head, row tile); its work is
+// one tile space: prefix tiles [0, ntp) (32 tokens each, up to the request's
+// length) followed by the draft tiles.  Workgroup `part` of a unit takes
+// tiles [part*T, part*T + T), T = P.tiles_per_part, and its W waves take
+// those tiles round-robin.  A wave loads a tile's K and V as whole token
+// rows (each 16-byte load instruction covers complete 128-byte lines:
+// measured 2x the tile rate of loading K in the MFMA operand layout, where
+// an instruction touches 32 rows), stages them in its own LDS area -- K
+// rows at a pitch for conflict-free A-operand reads, V rows at a pitch for
+// transpose reads -- and issues the next tile's loads as soon as the rows
+// are staged, so they are in flight during the current tile's MFMAs.
+// Masks, softmax and the hi/lo P.V product are tree_kernel's.  The waves
+// merge through LDS; with one part per unit (no workspace) wave 0 writes the
+// output, otherwise every part with tiles writes an FP32 partial per row,
+// slot (row, part), and merge_split_kernel combines them.
+template <int D, int W>
+__global__ __launch_bounds__(64 * W, 2) void tree_split_kernel(TreeParams P) {
+  constexpr int KS = D / 16;      // MFMA k-steps; also load instructions per tile
+  constexpr int DT = D / 32;      // 32-row output tiles over the head dimension
+  constexpr int KP = D + 8;       // halves per staged K row
+  constexpr int VP = D + 16;      // halves per staged V row
+  constexpr int LPR = D / 8;      // lanes per token row in a whole-row load
+  constexpr int RPI = 64 / LPR;   // token rows per load instruction
+  static_assert(RPI * KS == kTile, "KS whole-row loads cover a tile");
+  constexpr int STAGE = kTile * (KP + VP);  // halves per wave
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int g = lane >> 5;   // lane half
+  const int lr = lane & 31;  // tile column (query row) / token slot
+
+  const int zdim = P.hkv * P.row_tiles;
+  const int units = zdim * P.batch;
+  const int unit = blockIdx.x % units;  // (KV head, row tile) in the low bits
+  const int part = blockIdx.x / units;
+  const int z = unit % zdim;
+  const int b = unit / zdim;
+  const int kvh = z / P.row_tiles;
+  const int rt = z % P.row_tiles;
+  const int T = P.tiles_per_part;
+  const int tbeg = part * T;
+
+  // Page ids of this wave's tiles as vector loads (lane j: page j%2 of the
+  // wave's tile j/2, 32 tiles per register, the next 32 fetched a chunk
+  // ahead).  Scalar loads would share lgkmcnt with the LDS reads of every
+  // tile, whose waits would then also wait for the prefetched ids.  The ids
+  // are requested with the length (they do not depend on it; entries past
+  // the wave's tiles or the prefix are unused).
+  auto load_ids = [&](int chunk) {
+    const int it = tbeg + wave + W * (chunk * 32 + (lane >> 1));
+    const int pg = it * (kTile / BC_PAGE_SIZE) + (lane & 1);
+    return it < tbeg + T && pg < P.max_pages ? P.pages[(size_t)b * P.max_pages + pg] : -1;
+  };
+  int idv = load_ids(0);
+  int idv_next = -1;
+  if (T > 32 * W) idv_next = load_ids(1);
+  const int len = max(0, min(P.lengths[b], P.max_pages * BC_PAGE_SIZE));
+  const int ntp = (len + kTile - 1) / kTile;
+  const int ntot = ntp + (P.nodes + kTile - 1) / kTile;
+  const int tend = min(tbeg + T, ntot);
+  const int nmine = tend > tbeg + wave ? (tend - tbeg - wave + W - 1) / W : 0;
+
+  const int r = rt * 32 + lr;
+  const bool rvalid = r < P.rows;
+  const int node = rvalid ? r / P.group : 0;
+  const int h = kvh * P.group + (rvalid ? r % P.group : 0);
+
+  __shared__ __attribute__((aligned(16))) _Float16 s_stage[W * STAGE];
+  // Q^T B operand of the row tile, held by every wave: lane (g, lr) holds
+  // Q[row lr][16s + 8g .. +8] for each k-step s.  Rows past the tile's query
+  // rows hold zeros.
+  uint4 qB[KS];
+  {
+    const uint16_t* qp = P.dq + (((size_t)b * P.nodes + node) * P.hq + h) * D + 8 * g;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) qB[s] = rvalid ? ldg16(qp + 16 * s) : make_uint4(0, 0, 0, 0);
+  }
+  // The parent array in registers: lane i holds parent[i + 64c] (c < 4), so
+  // a wave walks ancestor chains with lane shuffles and needs no barrier.
+  static_assert(BC_MAX_TREE_NODES <= 256, "four parent registers per lane");
+  int parr[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const int i = lane + 64 * c;
+    parr[c] = i < P.nodes ? P.parent[(size_t)b * P.nodes + i] : -1;
+  }
+  auto parent_of = [&](int i) {  // i in [0, nodes)
+    if (P.nodes <= 64) return __shfl(parr[0], i, 64);
+    const int c0 = __shfl(parr[0], i & 63, 64), c1 = __shfl(parr[1], i & 63, 64);
+    const int c2 = __shfl(parr[2], i & 63, 64), c3 = __shfl(parr[3], i & 63, 64);
+    const int c = i >> 6;
+    return c == 0 ? c0 : c == 1 ? c1 : c == 2 ? c2 : c3;
+  };
+
+  _Float16* const ks = s_stage + wave * STAGE;
+  _Float16* const vs = ks + kTile * KP;
+  const int trG = lane >> 4, trj = lane & 15;
+  const _Float16* vtr = vs + (4 * (trG >> 1) + (trj >> 2)) * VP + 16 * (trG & 1) + 4 * (trj & 3);
+  // Whole-row load geometry: load s of a lane covers token row
+  // s*RPI + lane/LPR, dims 8*(lane%LPR) .. +8.
+  const int lrow = lane / LPR, lcol = 8 * (lane % LPR);
+  const size_t tok_stride = (size_t)P.hkv * D;
+
+  f32x16 acc[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+    for (int j = 0; j < 16; ++j) acc[dt][j] = 0.f;
+  float m = kNegInf, l = 0.f;
+
+  uint4 kreg[KS], vreg[KS];
+  uint32_t rowok = 0;  // bit s: this lane's row of load s is a valid token
+  // Issue the loads of this wave's tile `idx` (global tile it) from page ids
+  // ph; rows that are not valid tokens read an in-bounds row and are masked.
+  auto issue = [&](int idx, const int (&ph)[2]) {
+    const int it = tbeg + wave + W * idx;
+    rowok = 0;
+    if (it < ntp) {
+      const bool ok0 = ph[0] >= 0 && ph[0] < P.phys_pages;
+      const bool ok1 = ph[1] >= 0 && ph[1] < P.phys_pages;
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        const int tl = s * RPI + lrow;
+        const int q = tl / BC_PAGE_SIZE;  // compile-time per s when RPI divides 16
+        const bool ok = it * kTile + tl < len && (q ? ok1 : ok0);
+        rowok |= ok ? 1u << s : 0u;
+        const size_t phys = (size_t)(ok ? (q ? ph[1] : ph[0]) : 0);
+        const size_t off =
+            (phys * BC_PAGE_SIZE + tl % BC_PAGE_SIZE) * tok_stride + (size_t)kvh * D + lcol;
+        kreg[s] = ldg16(P.k + off);
+        vreg[s] = ldg16(P.v + off);
+      }
+    } else {
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        const int dn = (it - ntp) * kTile + s * RPI + lrow;
+        const bool ok = dn < P.nodes;
+        rowok |= ok ? 1u << s : 0u;
+        const size_t off = ok ? (((size_t)b * P.nodes + dn) * P.hkv + kvh) * D + lcol : lcol;
+        kreg[s] = ldg16(P.dk + off);
+        vreg[s] = ldg16(P.dv + off);
+      }
+    }
+  };
+
+  auto process = [&](int idx, const int (&ph)[2], const int (&next_ids)[2]) {
+    const int it = tbeg + wave + W * idx;
+    const bool is_draft = it >= ntp;
+    const int tbase = (is_draft ? it - ntp : it) * kTile;
+    // Valid token rows of the tile as a bit mask (bit i = token tbase + i):
+    // prefix tiles clip at the length and drop pages outside the pool;
+    // draft tiles take this row's ancestor-or-self set.
+    uint32_t okbits;
+    if (!is_draft) {
+      const int hi = min(max(len - tbase, 0), kTile);
+      okbits = (hi >= kTile ? ~0u : (1u << hi) - 1u) &
+               ((ph[0] >= 0 && ph[0] < P.phys_pages ? 0x0000ffffu : 0u) |
+                (ph[1] >= 0 && ph[1] < P.phys_pages ? 0xffff0000u : 0u));
+    } else {
+      // Lanes walk different chains, so the loop runs until every lane's
+      // walk has ended; a finished lane keeps cur = -1.
+      okbits = 0;
+      int cur = node;
+      for (int steps = 0; steps < P.nodes; ++steps) {
+        const bool live = cur >= 0 && cur < P.nodes;
+        if (!__builtin_amdgcn_ballot_w64(live)) break;
+        if (live && cur >= tbase && cur < tbase + kTile) okbits |= 1u << (cur - tbase);
+        const int nx = parent_of(live ? cur : 0);
+        cur = live ? nx : -1;
+      }
+    }
+    // Stage K and V rows; rows that are not valid tokens may hold any bits
+    // (NaN included): their weight is zero, so their V row must be zero.
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      const int tl = s * RPI + lrow;
+      *reinterpret_cast<uint4*>(ks + tl * KP + lcol) = kreg[s];
+      *reinterpret_cast<uint4*>(vs + tl * VP + lcol) =
+          (rowok >> s) & 1u ? vreg[s] : make_uint4(0, 0, 0, 0);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // The rows are in LDS: the next tile's loads go out now.
+    if (idx + 1 < nmine) issue(idx + 1, next_ids);
+
+    // ---- S^T = K Q^T, two independent MFMA chains over the k-steps ----
+    f32x16 sc0, sc1;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) sc0[j] = sc1[j] = 0.f;
+#pragma unroll
+    for (int s = 0; s < KS; s += 2) {
+      const uint4 k0 = *reinterpret_cast<const uint4*>(ks + lr * KP + 16 * s + 8 * g);
+      const uint4 k1 = *reinterpret_cast<const uint4*>(ks + lr * KP + 16 * (s + 1) + 8 * g);
+      sc0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_f16x8(k0), as_f16x8(qB[s]), sc0, 0, 0, 0);
+      sc1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_f16x8(k1), as_f16x8(qB[s + 1]), sc1, 0, 0,
+                                                   0);
+    }
+    // sc[j] holds token row 8*(j/4) + 4*g + j%4.
+    const uint32_t ob = okbits >> (4 * g);
+    float sv[16];
+    float tmax = kNegInf;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const bool ok = (ob >> (8 * (j >> 2) + (j & 3))) & 1u;
+      sv[j] = ok ? (sc0[j] + sc1[j]) * P.scale_log2 : kNegInf;
+      tmax = __builtin_fmaxf(tmax, sv[j]);
+    }
+    tmax = __builtin_fmaxf(tmax, shfl_xor_f(tmax, 32));
+    const float mnew = __builtin_fmaxf(m, tmax);
+    if (__builtin_amdgcn_ballot_w64(mnew > m + kRescaleSlack)) {
+      const float alpha = fast_exp2(m - safe_max(mnew));
+      l *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) acc[dt][j] *= alpha;
+      m = mnew;
+    }
+    const float mb = safe_max(m);
+    f16x8 pb[2], pl[2];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const float pr = fast_exp2(sv[j] - mb);
+      l += pr;
+      const _Float16 hi = (_Float16)pr;
+      pb[j >> 3][j & 7] = hi;
+      pl[j >> 3][j & 7] = (_Float16)(pr - (float)hi);
+    }
+    // ---- O^T += V^T P^T; A operand tokens 16st + 8hf + 4g + k, dim lr ----
+    // The MFMAs go round the DT accumulators, so consecutive ones are
+    // independent.
+    f16x8 av[DT][2];
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int st = 0; st < 2; ++st) {
+        const f16x4 lo = lds_read_tr(vtr + (16 * st) * VP + 32 * dt);
+        const f16x4 hi = lds_read_tr(vtr + (16 * st + 8) * VP + 32 * dt);
+        av[dt][st] = f16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      }
+#pragma unroll
+    for (int st = 0; st < 2; ++st)
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+        acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[dt][st], pb[st], acc[dt], 0, 0, 0);
+#pragma unroll
+    for (int st = 0; st < 2; ++st)
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+        acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[dt][st], pl[st], acc[dt], 0, 0, 0);
+    // The staging area is rewritten by the next tile.
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  };
+
+  auto ids_of = [&](int idx, int (&ph)[2]) {
+    if ((idx & 31) == 0 && idx > 0) {  // uniform: move to the next chunk of ids
+      idv = idv_next;
+      if (T > 32 * W * ((idx >> 5) + 1)) idv_next = load_ids((idx >> 5) + 1);
+    }
+    ph[0] = __builtin_amdgcn_readlane(idv, 2 * (idx & 31));
+    ph[1] = __builtin_amdgcn_readlane(idv, 2 * (idx & 31) + 1);
+  };
+  int cur[2] = {-1, -1};
+  if (nmine > 0) {
+    ids_of(0, cur);
+    issue(0, cur);
+  }
+  // The loads run one tile ahead of the MFMAs: while tile idx is processed,
+  // tile idx+1's rows are loading.
+  for (int idx = 0; idx < nmine; ++idx) {
+    int nxt[2] = {-1, -1};
+    if (idx + 1 < nmine) ids_of(idx + 1, nxt);
+    process(idx, cur, nxt);
+    cur[0] = nxt[0];
+    cur[1] = nxt[1];
+  }
+  l += shfl_xor_f(l, 32);  // both lane halves share m
+
+  // ---- merge the W waves through LDS in one step ----
+  // Every wave stores its state; after one barrier each thread combines the
+  // W states of its share of the tile (row mrow, DPT dims) and writes it.
+  constexpr int XP = D + 4;  // padded rows: a float4 access spreads over banks
+  static_assert(W * STAGE * 2 >= W * 32 * XP * 4, "merge buffer fits");
+  float* xacc = reinterpret_cast<float*>(s_stage);  // [W][32 rows][XP]
+  __shared__ float s_ml[W][32][2];
+  __syncthreads();  // the staging areas are reused below
+  {
+    float* dst = xacc + (size_t)wave * 32 * XP + (size_t)lr * XP;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int jq = 0; jq < 4; ++jq)
+        *reinterpret_cast<float4*>(dst + 32 * dt + 8 * jq + 4 * g) =
+            make_float4(acc[dt][4 * jq], acc[dt][4 * jq + 1], acc[dt][4 * jq + 2],
+                        acc[dt][4 * jq + 3]);
+    if (g == 0) {
+      s_ml[wave][lr][0] = m;
+      s_ml[wave][lr][1] = l;
+    }
+  }
+  __syncthreads();
+  constexpr int TPR = 2 * W;    // threads per row
+  constexpr int DPT = D / TPR;  // dims per thread
+  static_assert(DPT % 4 == 0, "float4 steps");
+  const int mrow = threadIdx.x / TPR;
+  const int md0 = (threadIdx.x % TPR) * DPT;
+  const int rr = rt * 32 + mrow;
+  if (rr >= P.rows) return;
+  float mw[W], mm = kNegInf;
+#pragma unroll
+  for (int w = 0; w < W; ++w) {
+    mw[w] = s_ml[w][mrow][0];
+    mm = __builtin_fmaxf(mm, mw[w]);
+  }
+  const float ms = safe_max(mm);  // all waves empty: every weight is 0
+  float ll = 0.f, o[DPT];
+#pragma unroll
+  for (int j = 0; j < DPT; ++j) o[j] = 0.f;
+#pragma unroll
+  for (int w = 0; w < W; ++w) {
+    const float wt = fast_exp2(mw[w] - ms);  // 0 for a wave without tiles
+    ll += wt * s_ml[w][mrow][1];
+    const float* src = xacc + ((size_t)w * 32 + mrow) * XP + md0;
+#pragma unroll
+    for (int j = 0; j < DPT; j += 4) {
+      const float4 v4 = *reinterpret_cast<const float4*>(src + j);
+      o[j] += wt * v4.x;
+      o[j + 1] += wt * v4.y;
+      o[j + 2] += wt * v4.z;
+      o[j + 3] += wt * v4.w;
+    }
+  }
+  const size_t orow = ((size_t)b * P.nodes + rr / P.group) * P.hq + kvh * P.group + rr % P.group;
+  if (P.parts == 1) {
+    const float inv = 1.f / ll;  // every row sees its own node: ll > 0
+    float* dst = P.out + orow * D + md0;
+#pragma unroll
+    for (int j = 0; j < DPT; j += 4)
+      *reinterpret_cast<float4*>(dst + j) =
+          make_float4(o[j] * inv, o[j + 1] * inv, o[j + 2] * inv, o[j + 3] * inv);
+  } else if (tbeg < ntot) {
+    const size_t slot = orow * P.parts + part;
+    float* dst = P.part_acc + slot * D + md0;
+#pragma unroll
+    for (int j = 0; j < DPT; j += 4)
+      *reinterpret_cast<float4*>(dst + j) = make_float4(o[j], o[j + 1], o[j + 2], o[j + 3]);
+    if (md0 == 0) *reinterpret_cast<float2*>(P.part_ml + 2 * slot) = make_float2(mm, ll);
+  }
+}
+
+// Combines tree_split_kernel's partials: one wave per output row (b, node,
+// h); the parts that held tiles, [0, nparts) with nparts from the request's
+// length, wrote slots (row, part).  Lane p holds slot p's (max, sum); the
+// weights are formed once and every lane accumulates its dims from eight
+// slots per step, all loads of a step issued before the first use.  The
+// (max, sum) loads and the first step's accumulators go out together with
+// the length, and slots past nparts are masked afterwards (their contents
+// are whatever the workspace held).
+template <int D>
+__global__ __launch_bounds__(256) void merge_split_kernel(TreeParams P) {
+  constexpr int PER = D / 64;
+  const int lane = threadIdx.x & 63;
+  const size_t row = (size_t)blockIdx.x * 4 + (threadIdx.x >> 6);  // (b*N+node)*Hq+h
+  if (row >= (size_t)P.batch * P.nodes * P.hq) return;
+  const int b = row / ((size_t)P.nodes * P.hq);
+  const int lraw = P.lengths[b];
+  const size_t base = row * P.parts;  // P.parts <= 64
+  auto load_slot = [&](int sidx, float (&v)[PER]) {
+    const float* src = P.part_acc + (base + sidx) * D + lane;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) v[j] = src[64 * j];
+  };
+  const float2 ml0 = *reinterpret_cast<const float2*>(P.part_ml + 2 * (base + min(lane, P.parts - 1)));
+  float v[8][PER];
+#pragma unroll
+  for (int u = 0; u < 8; ++u) load_slot(min(u, P.parts - 1), v[u]);
+#pragma unroll
+  for (int j = 0; j < PER; ++j)
+#pragma unroll
+    for (int u = 0; u < 8; ++u) asm volatile("" ::"v"(v[u][j]));
+  const int len = max(0, min(lraw, P.max_pages * BC_PAGE_SIZE));
+  const int ntot = (len + kTile - 1) / kTile + (P.nodes + kTile - 1) / kTile;
+  const int nparts = (ntot + P.tiles_per_part - 1) / P.tiles_per_part;  // >= 1
+  const bool written = lane < nparts;
+  const float mp = written ? ml0.x : kNegInf;
+  const float lp = written ? ml0.y : 0.f;
+  const float mm = wave_max(mp);
+  const float w = fast_exp2(mp - mm);  // every row sees its own node: mm finite
+  const float lsum = wave_sum(w * lp);
+  float a[PER];
+#pragma unroll
+  for (int j = 0; j < PER; ++j) a[j] = 0.f;
+  for (int i0 = 0; i0 < nparts; i0 += 8) {
+    if (i0 > 0) {
+#pragma unroll
+      for (int u = 0; u < 8; ++u) load_slot(min(i0 + u, nparts - 1), v[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      if (i0 + u < nparts) {  // uniform
+        const float wi = __builtin_bit_cast(
+            float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), i0 + u));
+#pragma unroll
+        for (int j = 0; j < PER; ++j) a[j] += wi * v[u][j];
+      }
+    }
+  }
+  const float inv = 1.f / lsum;
+#pragma unroll
+  for (int j = 0; j < PER; ++j) P.out[row * D + lane + 64 * j] = a[j] * inv;
 }
 
 // Row-sharing variant for trees of four or more row tiles per (request, KV
@@ -1362,6 +1780,78 @@ bool tree_ptrs_aligned(const bc_tree_inputs& in) {
          aligned16(in.draft_v) && aligned16(in.output);
 }
 
+// ---- tree_split_kernel: plan, workspace and launch ----
+
+struct SplitPlan {
+  int parts;  // workgroups per (request, KV head, row tile), <= 64
+  int tiles;  // 32-token tiles per workgroup (prefix then draft tiles)
+  int waves;  // waves per workgroup: 4 or 8
+};
+
+// Parts per unit and tiles per part for `cus` compute units, sized from the
+// page table's capacity (lengths stay on the device).  Eight-wave workgroups
+// (one per CU) with about one workgroup per CU over all units, every wave
+// with a tile; where that leaves CUs idle (few units: one request, short
+// prefixes), four-wave workgroups with one tile per wave, which spread the
+// tiles over twice the workgroups and merge in fewer LDS steps (one request
+// x 2048 tokens: 10.4 against 11.8 us; eight requests: 17.0 against 15.6).
+SplitPlan split_plan(const bc_shape& s, int nodes, int cus) {
+  const int group = s.query_heads / s.kv_heads;
+  const int row_tiles = (nodes * group + 31) / 32;
+  const long long units = (long long)s.batch * s.kv_heads * row_tiles;
+  const int max_tiles =
+      (s.max_pages * BC_PAGE_SIZE + kTile - 1) / kTile + (nodes + kTile - 1) / kTile;
+  auto plan_for = [&](int waves, long long want) {
+    if (want > 64) want = 64;
+    SplitPlan p{1, max_tiles, waves};
+    if (want < 2) return p;
+    int tiles = (int)((max_tiles + want - 1) / want);
+    if (tiles < waves) tiles = waves;
+    const int parts = (max_tiles + tiles - 1) / tiles;
+    return parts < 2 ? p : SplitPlan{parts, tiles, waves};
+  };
+  const long long u = units > 0 ? units : 1;
+  const SplitPlan eight = plan_for(8, cus / u);
+  if (eight.parts == 1 || eight.parts * u >= cus) return eight;
+  return plan_for(4, cus / u);
+}
+
+// Workspace of tree_split_kernel: P.parts (acc; max, sum) slots per output row.
+size_t split_workspace(const bc_shape& s, int nodes, const SplitPlan& plan, size_t* acc_bytes) {
+  if (plan.parts < 2) return 0;
+  const size_t slots = (size_t)s.batch * nodes * s.query_heads * plan.parts;
+  *acc_bytes = (slots * s.dim * sizeof(float) + 255) & ~(size_t)255;
+  return *acc_bytes + slots * 2 * sizeof(float);
+}
+
+template <int D>
+void launch_split_kernel(const TreeParams& P, int waves, dim3 grid, hipStream_t st) {
+  if (waves == 4)
+    tree_split_kernel<D, 4><<<grid, 256, 0, st>>>(P);
+  else
+    tree_split_kernel<D, 8><<<grid, 512, 0, st>>>(P);
+}
+
+hipError_t launch_split(TreeParams& P, int dim, const SplitPlan& plan, void* workspace,
+                        size_t acc_bytes, hipStream_t st) {
+  P.parts = plan.parts;
+  P.tiles_per_part = plan.tiles;
+  if (plan.parts > 1) {
+    P.part_acc = static_cast<float*>(workspace);
+    P.part_ml = reinterpret_cast<float*>(static_cast<char*>(workspace) + acc_bytes);
+  }
+  const dim3 grid((unsigned)((size_t)plan.parts * P.batch * P.hkv * P.row_tiles));
+  if (dim == 64) launch_split_kernel<64>(P, plan.waves, grid, st);
+  else launch_split_kernel<128>(P, plan.waves, grid, st);
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess || plan.parts < 2) return err;
+  const size_t rows = (size_t)P.batch * P.nodes * P.hq;
+  const dim3 mgrid((unsigned)((rows + 3) / 4));
+  if (dim == 64) merge_split_kernel<64><<<mgrid, 256, 0, st>>>(P);
+  else merge_split_kernel<128><<<mgrid, 256, 0, st>>>(P);
+  return hipGetLastError();
+}
+
 }  // namespace
 
 extern "C" int bc_tree_verify(bc_shape s, bc_tree_inputs in, int nodes,
@@ -1369,8 +1859,14 @@ extern "C" int bc_tree_verify(bc_shape s, bc_tree_inputs in, int nodes,
   if (!tree_args_ok(s, in, nodes)) return BC_ERROR_INVALID_VALUE;
   TreeParams P = make_params(s, in, nodes);
   P.prefix_parts = 0;
-  return launch_tree(P, s.dim, 1, false, tree_ptrs_aligned(in),
-                     reinterpret_cast<hipStream_t>(stream));
+  const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const bool vec = tree_ptrs_aligned(in);
+  if (vec && !rows_kernel_for(P.batch, P.hkv, P.row_tiles, false, bch::device_cus())) {
+    const int max_tiles =
+        (s.max_pages * BC_PAGE_SIZE + kTile - 1) / kTile + (nodes + kTile - 1) / kTile;
+    return launch_split(P, s.dim, SplitPlan{1, max_tiles, 8}, nullptr, 0, st);
+  }
+  return launch_tree(P, s.dim, 1, false, vec, st);
 }
 
 namespace {
@@ -1386,9 +1882,36 @@ bool grouped_for(const bc_shape& s, int nodes) {
   return group_kernel_for(s.batch, row_tiles);
 }
 
+bool split_for(const bc_shape& s, int nodes) {
+  const int row_tiles = (nodes * (s.query_heads / s.kv_heads) + 31) / 32;
+  return !rows_kernel_for(s.batch, s.kv_heads, row_tiles, true, bch::device_cus());
+}
+
+size_t ws_size(const bc_shape& s, int nodes, bool grouped) {
+  if (!grouped && split_for(s, nodes)) {
+    size_t a = 0;
+    return split_workspace(s, nodes, split_plan(s, nodes, bch::device_cus()), &a);
+  }
+  int chunk = 0, parts = 0;
+  return tree_workspace(s, nodes, grouped, &chunk, &parts);
+}
+
 int tree_ws_call(bc_shape s, bc_tree_inputs in, int nodes, bool grouped, void* workspace,
                  size_t workspace_bytes, bc_stream_t stream) {
   if (!tree_args_ok(s, in, nodes)) return BC_ERROR_INVALID_VALUE;
+  const bool vec = tree_ptrs_aligned(in);
+  // Tensors that are not 16-byte aligned take the element-wise single pass.
+  if (!vec) return bc_tree_verify(s, in, nodes, stream);
+  const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (!grouped && split_for(s, nodes)) {
+    SplitPlan plan = split_plan(s, nodes, bch::device_cus());
+    size_t acc = 0;
+    const size_t need = split_workspace(s, nodes, plan, &acc);
+    if (!workspace || need == 0 || workspace_bytes < need || !aligned16(workspace))
+      return bc_tree_verify(s, in, nodes, stream);
+    TreeParams P = make_params(s, in, nodes);
+    return launch_split(P, s.dim, plan, workspace, acc, st);
+  }
   int chunk = 0, parts = 0;
   const size_t need = tree_workspace(s, nodes, grouped, &chunk, &parts);
   if (!workspace || need == 0 || workspace_bytes < need || !aligned16(workspace))
@@ -1400,16 +1923,14 @@ int tree_ws_call(bc_shape s, bc_tree_inputs in, int nodes, bool grouped, void* w
   const size_t acc = (slots * s.dim * sizeof(float) + 255) & ~(size_t)255;
   P.part_acc = static_cast<float*>(workspace);
   P.part_ml = reinterpret_cast<float*>(static_cast<char*>(workspace) + acc);
-  return launch_tree(P, s.dim, parts + 1, grouped, tree_ptrs_aligned(in),
-                     reinterpret_cast<hipStream_t>(stream));
+  return launch_tree(P, s.dim, parts + 1, grouped, true, st);
 }
 
 }  // namespace
 
 extern "C" size_t bc_tree_verify_workspace_size(bc_shape s, int nodes) {
   if (!tree_shape_ok(s, nodes)) return 0;
-  int chunk = 0, parts = 0;
-  return tree_workspace(s, nodes, false, &chunk, &parts);
+  return ws_size(s, nodes, false);
 }
 
 extern "C" int bc_tree_verify_ws(bc_shape s, bc_tree_inputs in, int nodes,
@@ -1420,8 +1941,7 @@ extern "C" int bc_tree_verify_ws(bc_shape s, bc_tree_inputs in, int nodes,
 
 extern "C" size_t bc_tree_verify_shared_workspace_size(bc_shape s, int nodes) {
   if (!tree_shape_ok(s, nodes)) return 0;
-  int chunk = 0, parts = 0;
-  return tree_workspace(s, nodes, grouped_for(s, nodes), &chunk, &parts);
+  return ws_size(s, nodes, grouped_for(s, nodes));
 }
 
 extern "C" int bc_tree_verify_shared_ws(bc_shape s, bc_tree_inputs in, int nodes,

@@ -158,11 +158,12 @@ def test_long_sequences_many_partials(lens, oracle):
 
 def test_large_batch_takes_split_path(oracle):
     """128 sequences (one wave of flat ranges at 8 KV heads) run split with a
-    workspace; ragged lengths include empty sequences."""
+    workspace; ragged lengths include empty sequences.  The table holds more
+    than 512 tokens: shorter tables never split (src/paged_gqa.cu:135)."""
     torch.manual_seed(128)
     rng = np.random.default_rng(128)
     B, hq, hkv, d = 128, 32, 8, 128
-    lens = rng.integers(0, 401, size=B)
+    lens = rng.integers(0, 801, size=B)
     lens[::9] = 0
     maxp = -(-int(lens.max()) // 16)
     NB = sum(-(-int(n) // 16) for n in lens) + 8
