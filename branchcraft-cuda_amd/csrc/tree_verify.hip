@@ -511,17 +511,25 @@ __global__ __launch_bounds__(64 * W, 2) void tree_split_kernel(TreeParams P) {
   // tile, whose waits would then also wait for the prefetched ids.  The ids
   // are requested with the length (they do not depend on it; entries past
   // the wave's tiles or the prefix are unused).
+  const int ntd = (P.nodes + kTile - 1) / kTile;  // draft tiles come first
   auto load_ids = [&](int chunk) {
     const int it = tbeg + wave + W * (chunk * 32 + (lane >> 1));
-    const int pg = it * (kTile / BC_PAGE_SIZE) + (lane & 1);
-    return it < tbeg + T && pg < P.max_pages ? P.pages[(size_t)b * P.max_pages + pg] : -1;
+    const int pg = (it - ntd) * (kTile / BC_PAGE_SIZE) + (lane & 1);
+    return it < tbeg + T && pg >= 0 && pg < P.max_pages ? P.pages[(size_t)b * P.max_pages + pg]
+                                                         : -1;
   };
+  // Tile 0's ids as scalar loads: with the length they are all the first
+  // K/V loads wait for.
+  const int pg0 = (tbeg + wave - ntd) * (kTile / BC_PAGE_SIZE);
+  int cur[2] = {pg0 >= 0 && pg0 < P.max_pages ? P.pages[(size_t)b * P.max_pages + pg0] : -1,
+                pg0 >= 0 && pg0 + 1 < P.max_pages ? P.pages[(size_t)b * P.max_pages + pg0 + 1]
+                                                  : -1};
   int idv = load_ids(0);
   int idv_next = -1;
   if (T > 32 * W) idv_next = load_ids(1);
   const int len = max(0, min(P.lengths[b], P.max_pages * BC_PAGE_SIZE));
   const int ntp = (len + kTile - 1) / kTile;
-  const int ntot = ntp + (P.nodes + kTile - 1) / kTile;
+  const int ntot = ntd + ntp;
   const int tend = min(tbeg + T, ntot);
   const int nmine = tend > tbeg + wave ? (tend - tbeg - wave + W - 1) / W : 0;
 
@@ -532,23 +540,13 @@ __global__ __launch_bounds__(64 * W, 2) void tree_split_kernel(TreeParams P) {
 
   __shared__ __attribute__((aligned(16))) _Float16 s_stage[W * STAGE];
   // Q^T B operand of the row tile, held by every wave: lane (g, lr) holds
-  // Q[row lr][16s + 8g .. +8] for each k-step s.  Rows past the tile's query
-  // rows hold zeros.
+  // Q[row lr][16s + 8g .. +8] for each k-step s (rows past the tile's query
+  // rows: zeros).  The parent array in registers: lane i holds
+  // parent[i + 64c] (c < 4), so a wave walks ancestor chains with lane
+  // shuffles.  Both are loaded after tile 0's K/V (below).
   uint4 qB[KS];
-  {
-    const uint16_t* qp = P.dq + (((size_t)b * P.nodes + node) * P.hq + h) * D + 8 * g;
-#pragma unroll
-    for (int s = 0; s < KS; ++s) qB[s] = rvalid ? ldg16(qp + 16 * s) : make_uint4(0, 0, 0, 0);
-  }
-  // The parent array in registers: lane i holds parent[i + 64c] (c < 4), so
-  // a wave walks ancestor chains with lane shuffles and needs no barrier.
   static_assert(BC_MAX_TREE_NODES <= 256, "four parent registers per lane");
   int parr[4];
-#pragma unroll
-  for (int c = 0; c < 4; ++c) {
-    const int i = lane + 64 * c;
-    parr[c] = i < P.nodes ? P.parent[(size_t)b * P.nodes + i] : -1;
-  }
   auto parent_of = [&](int i) {  // i in [0, nodes)
     if (P.nodes <= 64) return __shfl(parr[0], i, 64);
     const int c0 = __shfl(parr[0], i & 63, 64), c1 = __shfl(parr[1], i & 63, 64);
@@ -578,9 +576,9 @@ __global__ __launch_bounds__(64 * W, 2) void tree_split_kernel(TreeParams P) {
   // Issue the loads of this wave's tile `idx` (global tile it) from page ids
   // ph; rows that are not valid tokens read an in-bounds row and are masked.
   auto issue = [&](int idx, const int (&ph)[2]) {
-    const int it = tbeg + wave + W * idx;
+    const int it = tbeg + wave + W * idx - ntd;  // prefix tile index when >= 0
     rowok = 0;
-    if (it < ntp) {
+    if (it >= 0) {
       const bool ok0 = ph[0] >= 0 && ph[0] < P.phys_pages;
       const bool ok1 = ph[1] >= 0 && ph[1] < P.phys_pages;
 #pragma unroll
@@ -598,7 +596,7 @@ __global__ __launch_bounds__(64 * W, 2) void tree_split_kernel(TreeParams P) {
     } else {
 #pragma unroll
       for (int s = 0; s < KS; ++s) {
-        const int dn = (it - ntp) * kTile + s * RPI + lrow;
+        const int dn = (it + ntd) * kTile + s * RPI + lrow;
         const bool ok = dn < P.nodes;
         rowok |= ok ? 1u << s : 0u;
         const size_t off = ok ? (((size_t)b * P.nodes + dn) * P.hkv + kvh) * D + lcol : lcol;
@@ -610,8 +608,8 @@ __global__ __launch_bounds__(64 * W, 2) void tree_split_kernel(TreeParams P) {
 
   auto process = [&](int idx, const int (&ph)[2], const int (&next_ids)[2]) {
     const int it = tbeg + wave + W * idx;
-    const bool is_draft = it >= ntp;
-    const int tbase = (is_draft ? it - ntp : it) * kTile;
+    const bool is_draft = it < ntd;
+    const int tbase = (is_draft ? it : it - ntd) * kTile;
     // Valid token rows of the tile as a bit mask (bit i = token tbase + i):
     // prefix tiles clip at the length and drop pages outside the pool;
     // draft tiles take this row's ancestor-or-self set.
@@ -728,10 +726,21 @@ __global__ __launch_bounds__(64 * W, 2) void tree_split_kernel(TreeParams P) {
     ph[0] = __builtin_amdgcn_readlane(idv, 2 * (idx & 31));
     ph[1] = __builtin_amdgcn_readlane(idv, 2 * (idx & 31) + 1);
   };
-  int cur[2] = {-1, -1};
-  if (nmine > 0) {
-    ids_of(0, cur);
-    issue(0, cur);
+  if (nmine > 0) issue(0, cur);
+  // Q and the parents load without branches (clamped addresses, then
+  // selects), so the first tile's waits need not cover them.
+  {
+    const uint16_t* qp = P.dq + (((size_t)b * P.nodes + node) * P.hq + h) * D + 8 * g;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) qB[s] = ldg16(qp + 16 * s);
+#pragma unroll
+    for (int s = 0; s < KS; ++s) qB[s] = rvalid ? qB[s] : make_uint4(0, 0, 0, 0);
+  }
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const int i = lane + 64 * c;
+    parr[c] = P.parent[(size_t)b * P.nodes + min(i, P.nodes - 1)];
+    parr[c] = i < P.nodes ? parr[c] : -1;
   }
   // The loads run one tile ahead of the MFMAs: while tile idx is processed,
   // tile idx+1's rows are loading.
