@@ -826,3 +826,49 @@ extern "C" int bc_packed_decode_ws(bc_shape s, const bc_half* q,
                        head_stride, slot_stride, kv_stride, scale, workspace,
                        workspace_bytes, stream);
 }
+
+// ---- bc_packed_decode_noalloc: the split workspace in a static array ----
+
+namespace {
+
+// File-scope device scratch for bc_packed_decode_noalloc: every device the
+// library runs on holds its own copy until the process ends.  Host code
+// never passes `scratch` itself to a kernel (in host code the name is a
+// host-side stand-in, not a device address); it uses the address
+// hipGetSymbolAddress returns for the current device.
+constexpr size_t kStaticScratchBytes = BC_STATIC_SCRATCH_BYTES;
+__device__ __align__(256) unsigned char scratch[kStaticScratchBytes];
+
+// Device address of `scratch` on the current device, looked up once per
+// device (with that device current) and cached; null if the lookup fails.
+void* static_scratch() {
+  static std::atomic<void*> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+  void* p = cache[dev].load(std::memory_order_acquire);
+  if (p) return p;
+  void* addr = nullptr;
+  if (hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch)) != hipSuccess || !addr) return nullptr;
+  cache[dev].store(addr, std::memory_order_release);  // the same address if two threads race
+  return addr;
+}
+
+}  // namespace
+
+extern "C" int bc_packed_decode_noalloc(bc_shape s, const bc_half* q,
+                                        const bc_half* packed_kv, const int32_t* pages,
+                                        const int32_t* lengths, bc_half* output,
+                                        long long block_stride, long long head_stride,
+                                        long long slot_stride, long long kv_stride,
+                                        float scale, bc_stream_t stream) {
+  if (!shape_ok(s)) return BC_ERROR_INVALID_VALUE;
+  const size_t need = bc_packed_decode_workspace_size(s);
+  if (need > kStaticScratchBytes) return BC_ERROR_OUT_OF_MEMORY;
+  void* ws = nullptr;
+  if (need > 0) {
+    ws = static_scratch();
+    if (!ws) return BC_ERROR_INVALID_VALUE;
+  }
+  return packed_common(s, q, packed_kv, pages, lengths, output, block_stride, head_stride,
+                       slot_stride, kv_stride, scale, ws, need, stream);
+}

@@ -18,6 +18,8 @@ LIB_PATH = Path(__file__).resolve().parent.parent / "lib" / "libbranchcraft_hip.
 
 BC_SUCCESS = 0
 BC_ERROR_INVALID_VALUE = 1
+BC_ERROR_OUT_OF_MEMORY = 2
+BC_STATIC_SCRATCH_BYTES = 16 << 20
 BC_PAGE_SIZE = 16
 BC_MAX_SPLITS = 256
 BC_MAX_TREE_NODES = 256
@@ -28,7 +30,7 @@ EXPORTED = (
     "bc_tree_verify_workspace_size", "bc_tree_verify_ws",
     "bc_tree_verify_shared_workspace_size", "bc_tree_verify_shared_ws", "bc_commit_path",
     "bc_commit_paths", "bc_copy_pages", "bc_packed_decode", "bc_packed_decode_workspace_size",
-    "bc_packed_decode_ws", "bc_version",
+    "bc_packed_decode_ws", "bc_packed_decode_noalloc", "bc_version",
 )
 
 
@@ -100,6 +102,10 @@ def load(path: str | Path | None = None) -> ctypes.CDLL:
                                         c_longlong, c_float, c_void_p, c_size_t,
                                         c_void_p]
     lib.bc_packed_decode_ws.restype = c_int
+    lib.bc_packed_decode_noalloc.argtypes = [Shape, c_void_p, c_void_p, c_void_p, c_void_p,
+                                             c_void_p, c_longlong, c_longlong, c_longlong,
+                                             c_longlong, c_float, c_void_p]
+    lib.bc_packed_decode_noalloc.restype = c_int
     lib.bc_version.argtypes = []
     lib.bc_version.restype = c_char_p
     if path is None:
@@ -111,7 +117,8 @@ def shape(batch, query_heads, kv_heads, dim, max_pages, physical_pages) -> Shape
     return Shape(batch, query_heads, kv_heads, dim, max_pages, physical_pages)
 
 
-__all__ = ["BC_SUCCESS", "BC_ERROR_INVALID_VALUE", "BC_PAGE_SIZE", "BC_MAX_SPLITS",
+__all__ = ["BC_SUCCESS", "BC_ERROR_INVALID_VALUE", "BC_ERROR_OUT_OF_MEMORY",
+           "BC_STATIC_SCRATCH_BYTES", "BC_PAGE_SIZE", "BC_MAX_SPLITS",
            "BC_MAX_TREE_NODES", "EXPORTED", "Shape", "Inputs", "Scratch",
            "TreeInputs", "load", "shape", "LIB_PATH", "POINTER", "c_int32",
            "c_uint16"]

@@ -30,6 +30,7 @@ typedef struct ihipStream_t* bc_stream_t;
 enum {
   BC_SUCCESS = 0,             /* hipSuccess */
   BC_ERROR_INVALID_VALUE = 1, /* hipErrorInvalidValue */
+  BC_ERROR_OUT_OF_MEMORY = 2, /* hipErrorOutOfMemory: a fixed scratch is too small */
 };
 
 /* Tokens per KV page (reference: kPageSize, include/branchcraft.hpp:8). */
@@ -224,6 +225,26 @@ int bc_packed_decode_ws(bc_shape shape, const bc_half* q,
                         long long slot_stride, long long kv_stride,
                         float scale, void* workspace, size_t workspace_bytes,
                         bc_stream_t stream);
+
+/* Bytes of the static device scratch of bc_packed_decode_noalloc (per GPU). */
+#define BC_STATIC_SCRATCH_BYTES (16u << 20)
+
+/* No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): bc_packed_decode_ws with its split workspace taken from
+ * a static device array of BC_STATIC_SCRATCH_BYTES (16 MiB) that each GPU
+ * holds until the process ends, so the call allocates nothing.  Shapes whose
+ * workspace (bc_packed_decode_workspace_size) exceeds that size return
+ * BC_ERROR_OUT_OF_MEMORY without launching; shapes that need none run
+ * unsplit.  Every call on one GPU shares that GPU's array: calls that overlap
+ * on one GPU (other streams, other host threads) race and must not be
+ * issued.  Otherwise the same arguments, rules and results as
+ * bc_packed_decode_ws. */
+int bc_packed_decode_noalloc(bc_shape shape, const bc_half* q, const bc_half* packed_kv,
+                             const int32_t* pages, const int32_t* lengths,
+                             bc_half* output, long long block_stride,
+                             long long head_stride, long long slot_stride,
+                             long long kv_stride, float scale, bc_stream_t stream);
 
 /* Library version string, for logs. */
 const char* bc_version(void);

@@ -151,6 +151,25 @@ def test_packed_rejects(strides, scale):
                                    None) == INVALID
 
 
+def test_noalloc_rejects_before_launch():
+    """bc_packed_decode_noalloc checks its arguments, then rejects a shape
+    whose split workspace exceeds the static scratch with
+    hipErrorOutOfMemory -- all before touching a pointer or the GPU."""
+    lib = capi.load()
+    strides = (2 * 16 * 8 * 128, 128, 8 * 128, 16 * 8 * 128)
+    ok = capi.Shape(64, 32, 8, 128, 256, 20000)
+    assert lib.bc_packed_decode_workspace_size(ok) <= capi.BC_STATIC_SCRATCH_BYTES
+    bad = capi.Shape(0, 32, 8, 128, 256, 20000)
+    assert lib.bc_packed_decode_noalloc(bad, FAKE, FAKE, FAKE, FAKE, FAKE, *strides, 0.1,
+                                        None) == INVALID
+    # 200 sequences of 128 query heads split, and their partials (30 MB)
+    # exceed the 16 MiB scratch
+    big = capi.Shape(200, 128, 8, 128, 256, 20000)
+    assert lib.bc_packed_decode_workspace_size(big) > capi.BC_STATIC_SCRATCH_BYTES
+    assert lib.bc_packed_decode_noalloc(big, FAKE, FAKE, FAKE, FAKE, FAKE, *strides, 0.1,
+                                        None) == capi.BC_ERROR_OUT_OF_MEMORY
+
+
 def test_auto_splits_policy():
     """Split decode runs (splits - 1) * batch + 1 flat page ranges, rounded
     down to whole waves of one workgroup per CU, each range served by

@@ -1,0 +1,100 @@
+"""bc_packed_decode_noalloc: bc_packed_decode_ws with its split workspace in
+the library's static device array (no allocation in the call).
+
+Two calls in a row through the C ABI -- benchmark config 5's shape, then a
+smaller batch that reuses (and must not be disturbed by) the first call's
+scratch contents -- each bit-identical to bc_packed_decode_ws on the same
+inputs with a workspace from the caching allocator, and within the packed
+decode tolerance of the CPU oracle.
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import branchcraft_capi as capi
+from oracle import oracle_c
+import gpu_helpers as G
+
+pytestmark = pytest.mark.gpu
+
+
+def _case(rng, batch, pool, hkv=8, hq=32, d=128, lo=128, hi=4096):
+    lens = rng.integers(lo, hi + 1, size=batch).astype(np.int32)
+    maxp = int(-(-lens.max() // 16))
+    perm = rng.permutation(pool).astype(np.int32)
+    pages = np.full((batch, maxp), -1, dtype=np.int32)
+    cur = 0
+    for i, n in enumerate(lens):
+        c = -(-int(n) // 16)
+        pages[i, :c] = perm[cur:cur + c]
+        cur += c
+    q = rng.standard_normal((batch, hq, d)).astype(np.float16)
+    return q, pages, lens
+
+
+def _run(entry, shape, q, cache, pages, lens, strides, scale):
+    tq, tp, tl = G.dev(q), G.dev(pages), G.dev(lens)
+    out = torch.full(q.shape, float("nan"), device="cuda", dtype=torch.float16)
+    L = G.lib()
+    if entry == "noalloc":
+        err = L.bc_packed_decode_noalloc(shape, tq.data_ptr(), cache.data_ptr(), tp.data_ptr(),
+                                         tl.data_ptr(), out.data_ptr(), *strides, scale,
+                                         G.stream())
+    else:
+        nbytes = L.bc_packed_decode_workspace_size(shape)
+        ws = torch.empty(max(1, nbytes), device="cuda", dtype=torch.uint8)
+        err = L.bc_packed_decode_ws(shape, tq.data_ptr(), cache.data_ptr(), tp.data_ptr(),
+                                    tl.data_ptr(), out.data_ptr(), *strides, scale,
+                                    ws.data_ptr(), nbytes, G.stream())
+    G.check(err, entry)
+    torch.cuda.synchronize()
+    return out.cpu().numpy()
+
+
+def test_noalloc_matches_workspace_entry_point_twice():
+    rng = np.random.default_rng(55)
+    pool, hkv, d = 20000, 8, 128
+    cache = torch.randn((pool, 2, 16, hkv, d), device="cuda", dtype=torch.float16)
+    strides = (cache.stride(0), cache.stride(3), cache.stride(2), cache.stride(1))
+    scale = 1 / math.sqrt(d)
+    host_cache = None
+    for batch in (64, 16):  # the second call is smaller
+        q, pages, lens = _case(rng, batch, pool)
+        shape = capi.Shape(batch, 32, hkv, d, pages.shape[1], pool)
+        need = G.lib().bc_packed_decode_workspace_size(shape)
+        assert 0 < need <= capi.BC_STATIC_SCRATCH_BYTES, need
+        got = _run("noalloc", shape, q, cache, pages, lens, strides, scale)
+        ref = _run("ws", shape, q, cache, pages, lens, strides, scale)
+        assert np.array_equal(got.view(np.uint16), ref.view(np.uint16)), f"batch {batch}"
+        if host_cache is None:
+            host_cache = cache.cpu().numpy()
+        exp32, _ = oracle_c.packed_decode(q, host_cache, pages, lens, strides, hkv, scale,
+                                          threads=16)
+        tol = G.f16_tolerance(exp32, 2e-3)
+        assert np.all(np.abs(got.astype(np.float32) - exp32) <= tol), f"batch {batch}"
+
+
+def test_noalloc_unsplit_shape_and_oversize_rejection():
+    """A short table runs unsplit (no scratch); an oversize shape returns
+    hipErrorOutOfMemory and leaves the output untouched."""
+    rng = np.random.default_rng(56)
+    pool, hkv, d = 64, 2, 64
+    cache = torch.randn((pool, 2, 16, hkv, d), device="cuda", dtype=torch.float16)
+    strides = (cache.stride(0), cache.stride(3), cache.stride(2), cache.stride(1))
+    q, pages, lens = _case(rng, 3, pool, hkv=hkv, hq=8, d=d, lo=1, hi=300)
+    shape = capi.Shape(3, 8, hkv, d, pages.shape[1], pool)
+    assert G.lib().bc_packed_decode_workspace_size(shape) == 0
+    got = _run("noalloc", shape, q, cache, pages, lens, strides, 0.125)
+    ref = _run("ws", shape, q, cache, pages, lens, strides, 0.125)
+    assert np.array_equal(got.view(np.uint16), ref.view(np.uint16))
+    big = capi.Shape(200, 128, 8, 128, 256, 20000)
+    out = torch.full((4,), 7.0, device="cuda", dtype=torch.float16)
+    err = G.lib().bc_packed_decode_noalloc(big, out.data_ptr(), out.data_ptr(), out.data_ptr(),
+                                           out.data_ptr(), out.data_ptr(), 1, 1, 1, 1, 0.1,
+                                           G.stream())
+    assert err == capi.BC_ERROR_OUT_OF_MEMORY
+    torch.cuda.synchronize()
+    assert torch.all(out == 7.0)
