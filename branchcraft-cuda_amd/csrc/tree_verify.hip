@@ -573,25 +573,36 @@ __global__ __launch_bounds__(64 * W, 2) void tree_split_kernel(TreeParams P) {
 
   uint4 kreg[KS], vreg[KS];
   uint32_t rowok = 0;  // bit s: this lane's row of load s is a valid token
-  // Issue the loads of this wave's tile `idx` (global tile it) from page ids
-  // ph; rows that are not valid tokens read an in-bounds row and are masked.
+  // Byte offset of this lane's 16 bytes in whole-row load j of a page (j <
+  // KS/2 loads per page: token row j*RPI + lrow, dims lcol .. +8); a prefix
+  // tile's loads are then a uniform page base plus these offsets.
+  constexpr int LPP = KS / 2;
+  unsigned loff[LPP];
+#pragma unroll
+  for (int j = 0; j < LPP; ++j)
+    loff[j] = (unsigned)((((size_t)(j * RPI + lrow)) * tok_stride + lcol) * sizeof(uint16_t));
+  const size_t page_elems = (size_t)BC_PAGE_SIZE * tok_stride;
+  // Issue the loads of this wave's tile `idx` from page ids ph.  Pages
+  // outside the pool read page 0 and rows past the length read their page's
+  // rows (all in bounds); both are masked.
   auto issue = [&](int idx, const int (&ph)[2]) {
     const int it = tbeg + wave + W * idx - ntd;  // prefix tile index when >= 0
     rowok = 0;
     if (it >= 0) {
-      const bool ok0 = ph[0] >= 0 && ph[0] < P.phys_pages;
-      const bool ok1 = ph[1] >= 0 && ph[1] < P.phys_pages;
+      const int tb = it * kTile;
 #pragma unroll
-      for (int s = 0; s < KS; ++s) {
-        const int tl = s * RPI + lrow;
-        const int q = tl / BC_PAGE_SIZE;  // compile-time per s when RPI divides 16
-        const bool ok = it * kTile + tl < len && (q ? ok1 : ok0);
-        rowok |= ok ? 1u << s : 0u;
-        const size_t phys = (size_t)(ok ? (q ? ph[1] : ph[0]) : 0);
-        const size_t off =
-            (phys * BC_PAGE_SIZE + tl % BC_PAGE_SIZE) * tok_stride + (size_t)kvh * D + lcol;
-        kreg[s] = ldg16(P.k + off);
-        vreg[s] = ldg16(P.v + off);
+      for (int q = 0; q < 2; ++q) {
+        const bool okp = ph[q] >= 0 && ph[q] < P.phys_pages;
+        const size_t base = (size_t)(okp ? ph[q] : 0) * page_elems + (size_t)kvh * D;
+        const char* kb = reinterpret_cast<const char*>(P.k + base);
+        const char* vb = reinterpret_cast<const char*>(P.v + base);
+#pragma unroll
+        for (int j = 0; j < LPP; ++j) {
+          const int s = q * LPP + j;
+          rowok |= okp && tb + s * RPI + lrow < len ? 1u << s : 0u;
+          kreg[s] = *reinterpret_cast<const uint4*>(kb + loff[j]);
+          vreg[s] = *reinterpret_cast<const uint4*>(vb + loff[j]);
+        }
       }
     } else {
 #pragma unroll
@@ -680,15 +691,18 @@ __global__ __launch_bounds__(64 * W, 2) void tree_split_kernel(TreeParams P) {
         for (int j = 0; j < 16; ++j) acc[dt][j] *= alpha;
       m = mnew;
     }
+    // P splits into an FP16 hi part -- p with the low 13 mantissa bits
+    // cleared, exact in FP16 for p in [2^-14, 2^8] -- and lo = p - hi (exact
+    // in FP32, then rounded to FP16), so P.V carries ~21 bits of P.
     const float mb = safe_max(m);
     f16x8 pb[2], pl[2];
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
       const float pr = fast_exp2(sv[j] - mb);
       l += pr;
-      const _Float16 hi = (_Float16)pr;
-      pb[j >> 3][j & 7] = hi;
-      pl[j >> 3][j & 7] = (_Float16)(pr - (float)hi);
+      const float hi = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, pr) & 0xffffe000u);
+      pb[j >> 3][j & 7] = (_Float16)hi;
+      pl[j >> 3][j & 7] = (_Float16)(pr - hi);
     }
     // ---- O^T += V^T P^T; A operand tokens 16st + 8hf + 4g + k, dim lr ----
     // The MFMAs go round the DT accumulators, so consecutive ones are

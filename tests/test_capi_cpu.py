@@ -184,6 +184,9 @@ def test_auto_splits_policy():
     # short contexts whose (sequence, head block) workgroups fit the CUs run
     # unsplit: eight waves share each sequence's pages, no merge kernel
     assert lib.bc_auto_splits(_shape(batch=1), 512, 256) == 1
+    assert lib.bc_auto_splits(_shape(batch=1), 768, 256) == 1
+    assert lib.bc_auto_splits(_shape(batch=1), 769, 256) > 1
+    assert lib.bc_auto_splits(_shape(batch=16), 1024, 256) > 1
     assert lib.bc_auto_splits(_shape(batch=32), 1024, 256) == 1
     assert lib.bc_auto_splits(_shape(batch=33), 1024, 256) > 1
     assert lib.bc_auto_splits(_shape(batch=1), 1025, 256) > 1
@@ -206,11 +209,14 @@ def test_workspace_sizes():
     lib = capi.load()
     c5 = capi.Shape(64, 32, 8, 128, 256, 20000)
     assert lib.bc_packed_decode_workspace_size(c5) > 0
-    # Page tables of at most 1024 tokens whose (sequence, head block)
-    # workgroups fit the CUs run unsplit: no workspace.
+    # Page tables of at most 768 tokens (1024 for batches whose (sequence,
+    # head block) workgroups fill more than half the CUs) whose workgroups
+    # fit the CUs run unsplit: no workspace.
     assert lib.bc_packed_decode_workspace_size(capi.Shape(4, 32, 8, 128, 8, 64)) == 0
-    assert lib.bc_packed_decode_workspace_size(capi.Shape(4, 32, 8, 128, 64, 64)) == 0
-    assert lib.bc_packed_decode_workspace_size(capi.Shape(4, 32, 8, 128, 65, 64)) > 0
+    assert lib.bc_packed_decode_workspace_size(capi.Shape(4, 32, 8, 128, 48, 64)) == 0
+    assert lib.bc_packed_decode_workspace_size(capi.Shape(4, 32, 8, 128, 49, 64)) > 0
+    assert lib.bc_packed_decode_workspace_size(capi.Shape(32, 32, 8, 128, 64, 64)) == 0
+    assert lib.bc_packed_decode_workspace_size(capi.Shape(32, 32, 8, 128, 65, 64)) > 0
     # Tables below 512 tokens never split; from 512 on, batches whose
     # workgroups outnumber the CUs do.
     assert lib.bc_packed_decode_workspace_size(capi.Shape(64, 32, 8, 128, 8, 64)) == 0
