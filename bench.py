@@ -337,9 +337,8 @@ def tree_setup(cx, batch, prefix, seed, nodes=7):
     return f
 
 
-def tree_call(cx, f, workspace=True, shared=False):
-    """bc_tree_verify_ws (workspace), bc_tree_verify, or with shared=True the
-    shared-prefix entry point bc_tree_verify_shared_ws."""
+def tree_call(cx, f, workspace=True):
+    """bc_tree_verify_ws (workspace) or bc_tree_verify."""
     capi = cx.capi
     shape = capi.Shape(f["batch"], f["hq"], f["hkv"], f["d"], f["pages"].shape[1], f["pool"])
     prefix = capi.Inputs(None, f["k"].data_ptr(), f["v"].data_ptr(), f["pages"].data_ptr(),
@@ -348,15 +347,12 @@ def tree_call(cx, f, workspace=True, shared=False):
                           f["parent"].data_ptr(), f["out"].data_ptr())
     lib, st, n = cx.lib, cx.stream(), f["n"]
     if workspace:
-        size_fn, entry = ((lib.bc_tree_verify_shared_workspace_size, lib.bc_tree_verify_shared_ws)
-                          if shared else (lib.bc_tree_verify_workspace_size, lib.bc_tree_verify_ws))
-        nb = size_fn(shape, n)
-        key = "ws_shared" if shared else "ws"
-        f[key] = cx.torch.empty(max(1, nb), device="cuda", dtype=cx.torch.uint8)
-        ws = f[key].data_ptr()
+        nb = lib.bc_tree_verify_workspace_size(shape, n)
+        f["ws"] = cx.torch.empty(max(1, nb), device="cuda", dtype=cx.torch.uint8)
+        ws = f["ws"].data_ptr()
 
         def call():
-            err = entry(shape, ins, n, ws, nb, st)
+            err = lib.bc_tree_verify_ws(shape, ins, n, ws, nb, st)
             if err:
                 raise RuntimeError(f"tree_verify workspace call error {err}")
     else:
@@ -421,8 +417,7 @@ def bench_tree(cx, batch, prefix, seed, with_expanded, nodes=7):
     t = cx.torch
     f = tree_setup(cx, batch, prefix, seed, nodes)
     res = {}
-    calls = {"ws": tree_call(cx, f, True), "single": tree_call(cx, f, False),
-             "shared": tree_call(cx, f, True, shared=True)}
+    calls = {"ws": tree_call(cx, f, True), "single": tree_call(cx, f, False)}
     outs = {}
     for name, fn in calls.items():
         res[f"tree_{name}_us"] = round(median_us(t, fn), 3)
@@ -430,9 +425,6 @@ def bench_tree(cx, batch, prefix, seed, with_expanded, nodes=7):
         t.cuda.synchronize()
         outs[name] = f["out"].clone()
     res["tree_ws_vs_single_maxdiff"] = float((outs["ws"] - outs["single"]).abs().max())
-    res["tree_shared_vs_ws_maxdiff"] = float((outs["shared"] - outs["ws"]).abs().max())
-    if res["tree_shared_vs_ws_maxdiff"] > 2e-3:
-        raise RuntimeError("bc_tree_verify_shared_ws and bc_tree_verify_ws disagree")
     unique, flops = tree_metrics(f)
     tree_us = min(res["tree_ws_us"], res["tree_single_us"])
     res.update(tree_us=tree_us, tree_bytes=unique, tree_gflop=round(flops / 1e9, 4),
@@ -626,8 +618,8 @@ def main():
         print(f"[bench] C3 {results['c3_tree']}", file=sys.stderr, flush=True)
     if want("tl"):
         # A large draft tree (beyond the benchmark configs): 8 requests x 256
-        # nodes over a 2048-token shared prefix, where the verifier shares each
-        # K/V tile between four row tiles.
+        # nodes over a 2048-token shared prefix, where tree_rows_kernel shares
+        # each K/V tile between four row tiles.
         results["tree_large"] = bench_tree(cx, 8, 2048, 4, with_expanded=False, nodes=256)
         print(f"[bench] tree 8 x 2048 x 256 nodes {results['tree_large']}", file=sys.stderr,
               flush=True)
@@ -662,7 +654,6 @@ def main():
             "decode_us_per_call": round(ms * 1e3, 3),
             "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 1),
             "tree_verify_us_8x2048": results.get("c3_tree", {}).get("tree_us"),
-            "tree_verify_shared_us_8x2048": results.get("c3_tree", {}).get("tree_shared_us"),
             "device": props.name,
             "cus": cx.cus,
         },

@@ -44,13 +44,11 @@ bc_half* hptr_mut(at::Tensor& t) {
   return reinterpret_cast<bc_half*>(t.data_ptr<at::Half>());
 }
 
-// Reference: tree_verify_cuda, bindings/torch_ops.cpp:22-67.  `shared`
-// selects bc_tree_verify_shared_ws (requests forked from one prefix; no
-// reference counterpart) with the same checks and output.
-at::Tensor tree_verify_impl(const at::Tensor& q, const at::Tensor& prefix_k,
-                            const at::Tensor& prefix_v, const at::Tensor& pages,
-                            const at::Tensor& lengths, const at::Tensor& draft_k,
-                            const at::Tensor& draft_v, const at::Tensor& parent, bool shared) {
+// Reference: tree_verify_cuda, bindings/torch_ops.cpp:22-67.
+at::Tensor tree_verify_hip(const at::Tensor& q, const at::Tensor& prefix_k,
+                           const at::Tensor& prefix_v, const at::Tensor& pages,
+                           const at::Tensor& lengths, const at::Tensor& draft_k,
+                           const at::Tensor& draft_v, const at::Tensor& parent) {
   check_dev_contig(q, "q", at::kHalf);
   check_dev_contig(prefix_k, "prefix_k", at::kHalf);
   check_dev_contig(prefix_v, "prefix_v", at::kHalf);
@@ -91,34 +89,14 @@ at::Tensor tree_verify_impl(const at::Tensor& q, const at::Tensor& prefix_k,
                    lengths.data_ptr<int>(), nullptr};
   bc_tree_inputs in{prefix, hptr(q), hptr(draft_k), hptr(draft_v),
                     parent.data_ptr<int>(), output.data_ptr<float>()};
-  const size_t ws_bytes = shared ? bc_tree_verify_shared_workspace_size(shape, int(nodes))
-                                 : bc_tree_verify_workspace_size(shape, int(nodes));
+  const size_t ws_bytes = bc_tree_verify_workspace_size(shape, int(nodes));
   at::Tensor ws;
   if (ws_bytes > 0)
     ws = at::empty({int64_t(ws_bytes)}, q.options().dtype(at::kByte));
   void* const wsp = ws_bytes ? ws.data_ptr() : nullptr;
-  check_launch(shared ? bc_tree_verify_shared_ws(shape, in, int(nodes), wsp, ws_bytes,
-                                                 current_stream())
-                      : bc_tree_verify_ws(shape, in, int(nodes), wsp, ws_bytes,
-                                          current_stream()),
-               shared ? "tree_verify_shared" : "tree_verify");
+  check_launch(bc_tree_verify_ws(shape, in, int(nodes), wsp, ws_bytes, current_stream()),
+               "tree_verify");
   return output;
-}
-
-at::Tensor tree_verify_hip(const at::Tensor& q, const at::Tensor& prefix_k,
-                           const at::Tensor& prefix_v, const at::Tensor& pages,
-                           const at::Tensor& lengths, const at::Tensor& draft_k,
-                           const at::Tensor& draft_v, const at::Tensor& parent) {
-  return tree_verify_impl(q, prefix_k, prefix_v, pages, lengths, draft_k, draft_v, parent,
-                          false);
-}
-
-at::Tensor tree_verify_shared_hip(const at::Tensor& q, const at::Tensor& prefix_k,
-                                  const at::Tensor& prefix_v, const at::Tensor& pages,
-                                  const at::Tensor& lengths, const at::Tensor& draft_k,
-                                  const at::Tensor& draft_v, const at::Tensor& parent) {
-  return tree_verify_impl(q, prefix_k, prefix_v, pages, lengths, draft_k, draft_v, parent,
-                          true);
 }
 
 // Compute units of a device, cached (an immutable attribute).
@@ -365,7 +343,6 @@ TORCH_LIBRARY(branchcraft, m) {
   m.def("commit_path_(Tensor(a!) cache_k, Tensor(b!) cache_v, Tensor draft_k, Tensor draft_v, Tensor path_nodes, Tensor dest_pages, Tensor dest_slots, int request) -> ()");
   m.def("copy_pages_(Tensor(a!) cache_k, Tensor(b!) cache_v, Tensor src_pages, Tensor dst_pages) -> ()");
   m.def("commit_paths_(Tensor(a!) cache_k, Tensor(b!) cache_v, Tensor draft_k, Tensor draft_v, Tensor requests, Tensor path_nodes, Tensor dest_pages, Tensor dest_slots) -> ()");
-  m.def("tree_verify_shared(Tensor q, Tensor prefix_k, Tensor prefix_v, Tensor pages, Tensor lengths, Tensor draft_k, Tensor draft_v, Tensor parent) -> Tensor");
   m.def("paged_decode(Tensor q, Tensor k, Tensor v, Tensor pages, Tensor lengths, int splits=0) -> Tensor");
 }
 
@@ -375,6 +352,5 @@ TORCH_LIBRARY_IMPL(branchcraft, CUDA, m) {
   m.impl("commit_path_", commit_path_hip);
   m.impl("copy_pages_", copy_pages_hip);
   m.impl("commit_paths_", commit_paths_hip);
-  m.impl("tree_verify_shared", tree_verify_shared_hip);
   m.impl("paged_decode", paged_decode_hip);
 }

@@ -11,32 +11,28 @@
 //   O^T[D x 32 rows]     += V^T[D x 32 tok] . P^T[32 tok x 32 rows]
 //
 // P enters the second product as an FP16 hi/lo pair (two MFMAs), so the
-// only rounding left is the FP32 accumulation.
+// only rounding left is the FP32 accumulation.  The S^T accumulator layout
+// is, lane for lane, the B operand of the P.V product once the token order
+// inside a 16-token step is permuted, so P never leaves registers; V^T is
+// read from LDS with ds_read_b64_tr_b16.  The draft nodes form extra 32-token
+// tiles whose scores are masked by the row's ancestor set, walked from the
+// parent array (at most N steps, stopping at a parent outside [0, N)).
 //
-// K tiles feed the A operand straight from HBM (16 contiguous bytes per lane
-// per MFMA).  The S^T accumulator layout is, lane for lane, the B operand of
-// the P.V product once the token order inside a 16-token step is permuted
-// (token tau(s,g,i) = 16s + 8*(i/4) + 4g + i%4 for lane half g), so P never
-// leaves registers.  V is staged row-major in LDS (per wave, 32 tokens x D,
-// one 16-byte store per lane and k-step) and the V^T A operand is read with
-// ds_read_b64_tr_b16: inside each 16-lane group, lane i receives element
-// i%4 of the 8-byte chunks addressed by lanes i/4 + 4k (k = 0..3), so lanes
-// that address [token tb + j/4][dim db + 4*(j%4)] yield V[tb + k][db + i].  The draft nodes form
-// extra 32-token tiles whose scores are masked by the row's ancestor set,
-// walked from the parent array held in LDS (at most N steps, stopping at a
-// parent outside [0, N)).
-//
-// Work unit: (request, KV head, row tile, prefix chunk).  Four waves take
-// 32-token tiles round-robin and merge their online-softmax states through
-// LDS; with a workspace, chunks write FP32 partials that merge_tree_kernel
-// combines.  Workgroup ids put (KV head, row tile) in the low bits, so the
-// requests that share prefix pages run on the same XCD and reuse its L2.
-// Large trees, whose row tiles would need two or more such workgroups per
-// CU, run tree_rows_kernel instead: its unit is (request, KV head, four row
-// tiles, prefix chunk), and each K/V tile is loaded once for all four.
-// bc_tree_verify_shared_ws, for requests forked from one prefix, runs
-// tree_group_kernel: its unit is (four requests, KV head, prefix chunk), and
-// each tile is loaded once for the four requests where their pages agree.
+// Kernels:
+//  - tree_split_kernel (16-byte aligned tensors, the common path): unit =
+//    (request, KV head, row tile); each of a unit's `parts` workgroups takes
+//    a range of 32-token tiles (draft tiles first, then prefix tiles), its
+//    waves take the range's tiles round-robin with whole-row 16-byte loads
+//    staged through per-wave LDS, and merge through LDS; with parts > 1
+//    merge_split_kernel combines the FP32 partials.  Workgroup ids put
+//    (KV head, row tile) in the low bits, so requests that share prefix
+//    pages run on the same XCD and reuse its L2.
+//  - tree_rows_kernel: trees of many row tiles per (request, KV head), whose
+//    units already fill the CUs: four waves take four row tiles and walk the
+//    same K/V tiles, loaded once per workgroup; merge_tree_kernel combines
+//    its prefix chunks.
+//  - tree_kernel: the single pass for tensors that are not 16-byte aligned
+//    (element-wise loads and stores).
 #include "bc_device.h"
 #include "bc_host.h"
 
@@ -463,6 +459,136 @@ __global__ __launch_bounds__(kThreads, 2) void tree_kernel(TreeParams P) {
   }
 }
 
+// ---- per-tile pieces of tree_split_kernel ----
+
+// Valid tokens of a prefix tile: the first `valid` rows (clipped to
+// [0, 32]), minus the 16-row halves whose page id lies outside the pool.
+__device__ __forceinline__ uint32_t prefix_bits(int valid, int id0, int id1, int phys) {
+  const int hi = min(max(valid, 0), kTile);
+  return (hi >= kTile ? ~0u : (1u << hi) - 1u) &
+         ((id0 >= 0 && id0 < phys ? 0x0000ffffu : 0u) |
+          (id1 >= 0 && id1 < phys ? 0xffff0000u : 0u));
+}
+
+// parent[i] for i in [0, nodes) from the parent registers (lane i of
+// register c holds parent[i + 64c]).
+__device__ __forceinline__ int parent_at(const int (&parr)[4], int nodes, int i) {
+  if (nodes <= 64) return __shfl(parr[0], i, 64);
+  const int c0 = __shfl(parr[0], i & 63, 64), c1 = __shfl(parr[1], i & 63, 64);
+  const int c2 = __shfl(parr[2], i & 63, 64), c3 = __shfl(parr[3], i & 63, 64);
+  const int c = i >> 6;
+  return c == 0 ? c0 : c == 1 ? c1 : c == 2 ? c2 : c3;
+}
+
+// Valid tokens of the draft tile starting at node tbase for the lane's
+// query row: its node and that node's ancestors.  Lanes walk different
+// chains, so the loop runs until every lane's walk has ended (a parent
+// outside [0, nodes) ends it; at most `nodes` steps).
+__device__ __forceinline__ uint32_t ancestor_bits(const int (&parr)[4], int nodes, int node,
+                                                  int tbase) {
+  uint32_t okbits = 0;
+  int cur = node;
+  for (int steps = 0; steps < nodes; ++steps) {
+    const bool live = cur >= 0 && cur < nodes;
+    if (!__builtin_amdgcn_ballot_w64(live)) break;
+    if (live && cur >= tbase && cur < tbase + kTile) okbits |= 1u << (cur - tbase);
+    const int nx = parent_at(parr, nodes, live ? cur : 0);
+    cur = live ? nx : -1;
+  }
+  return okbits;
+}
+
+// One 32-token tile staged in LDS (K rows at a pitch of D + 8 halves, V
+// rows at D + 16): S^T = K Q^T as two MFMA chains over the k-steps, the
+// masked online-softmax update of (m, l, acc), and O^T += V^T P^T with P as
+// an FP16 hi/lo pair.  kr is this lane's K row (token lr), vtr its
+// transpose-read address in the V rows, qB the Q^T B operand and okbits the
+// valid tokens of the lane's query row.
+template <int D>
+__device__ __forceinline__ void tile_math(const _Float16* kr, const _Float16* vtr,
+                                          const uint4 (&qB)[D / 16], uint32_t okbits,
+                                          float scale_log2, int g, f32x16 (&acc)[D / 32],
+                                          float& m, float& l) {
+  constexpr int KS = D / 16;
+  constexpr int DT = D / 32;
+  constexpr int VP = D + 16;
+  f32x16 sc0, sc1;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) sc0[j] = sc1[j] = 0.f;
+#pragma unroll
+  for (int s = 0; s < KS; s += 2) {
+    const uint4 k0 = *reinterpret_cast<const uint4*>(kr + 16 * s + 8 * g);
+    const uint4 k1 = *reinterpret_cast<const uint4*>(kr + 16 * (s + 1) + 8 * g);
+    sc0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_f16x8(k0), as_f16x8(qB[s]), sc0, 0, 0, 0);
+    sc1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_f16x8(k1), as_f16x8(qB[s + 1]), sc1, 0, 0,
+                                                 0);
+  }
+  // sc[j] holds token row 8*(j/4) + 4*g + j%4.
+  const uint32_t ob = okbits >> (4 * g);
+  float sv[16];
+  float tmax = kNegInf;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const bool ok = (ob >> (8 * (j >> 2) + (j & 3))) & 1u;
+    sv[j] = ok ? (sc0[j] + sc1[j]) * scale_log2 : kNegInf;
+    tmax = __builtin_fmaxf(tmax, sv[j]);
+  }
+  tmax = __builtin_fmaxf(tmax, shfl_xor_f(tmax, 32));
+  const float mnew = __builtin_fmaxf(m, tmax);
+  if (__builtin_amdgcn_ballot_w64(mnew > m + kRescaleSlack)) {
+    const float alpha = fast_exp2(m - safe_max(mnew));
+    l *= alpha;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) acc[dt][j] *= alpha;
+    m = mnew;
+  }
+  // P splits into an FP16 hi part -- p with the low 13 mantissa bits
+  // cleared, exact in FP16 for p in [2^-14, 2^8] -- and lo = p - hi (exact
+  // in FP32, then rounded to FP16), so P.V carries ~21 bits of P.
+  const float mb = safe_max(m);
+  f16x8 pb[2], pl[2];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const float pr = fast_exp2(sv[j] - mb);
+    l += pr;
+    const float hi = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, pr) & 0xffffe000u);
+    pb[j >> 3][j & 7] = (_Float16)hi;
+    pl[j >> 3][j & 7] = (_Float16)(pr - hi);
+  }
+  // ---- O^T += V^T P^T; A operand tokens 16st + 8hf + 4g + k, dim lr ----
+  // The MFMAs go round the DT accumulators, so consecutive ones are
+  // independent.
+  f16x8 av[DT][2];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+    for (int st = 0; st < 2; ++st) {
+      const f16x4 lo = lds_read_tr(vtr + (16 * st) * VP + 32 * dt);
+      const f16x4 hi = lds_read_tr(vtr + (16 * st + 8) * VP + 32 * dt);
+      av[dt][st] = f16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    }
+#pragma unroll
+  for (int st = 0; st < 2; ++st)
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+      acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[dt][st], pb[st], acc[dt], 0, 0, 0);
+#pragma unroll
+  for (int st = 0; st < 2; ++st)
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+      acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[dt][st], pl[st], acc[dt], 0, 0, 0);
+}
+
+// Wave-local LDS handoff: this wave's LDS writes are visible to its own
+// later reads (and its reads done before its later writes).
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 // Split tree verification.  Unit = (request, KV head, row tile); its work is
 // one tile space: prefix tiles [0, ntp) (32 tokens each, up to the request's
 // length) followed by the draft tiles.  Workgroup `part` of a unit takes
@@ -547,13 +673,6 @@ __global__ __launch_bounds__(64 * W, 2) void tree_split_kernel(TreeParams P) {
   uint4 qB[KS];
   static_assert(BC_MAX_TREE_NODES <= 256, "four parent registers per lane");
   int parr[4];
-  auto parent_of = [&](int i) {  // i in [0, nodes)
-    if (P.nodes <= 64) return __shfl(parr[0], i, 64);
-    const int c0 = __shfl(parr[0], i & 63, 64), c1 = __shfl(parr[1], i & 63, 64);
-    const int c2 = __shfl(parr[2], i & 63, 64), c3 = __shfl(parr[3], i & 63, 64);
-    const int c = i >> 6;
-    return c == 0 ? c0 : c == 1 ? c1 : c == 2 ? c2 : c3;
-  };
 
   _Float16* const ks = s_stage + wave * STAGE;
   _Float16* const vs = ks + kTile * KP;
@@ -624,25 +743,9 @@ __global__ __launch_bounds__(64 * W, 2) void tree_split_kernel(TreeParams P) {
     // Valid token rows of the tile as a bit mask (bit i = token tbase + i):
     // prefix tiles clip at the length and drop pages outside the pool;
     // draft tiles take this row's ancestor-or-self set.
-    uint32_t okbits;
-    if (!is_draft) {
-      const int hi = min(max(len - tbase, 0), kTile);
-      okbits = (hi >= kTile ? ~0u : (1u << hi) - 1u) &
-               ((ph[0] >= 0 && ph[0] < P.phys_pages ? 0x0000ffffu : 0u) |
-                (ph[1] >= 0 && ph[1] < P.phys_pages ? 0xffff0000u : 0u));
-    } else {
-      // Lanes walk different chains, so the loop runs until every lane's
-      // walk has ended; a finished lane keeps cur = -1.
-      okbits = 0;
-      int cur = node;
-      for (int steps = 0; steps < P.nodes; ++steps) {
-        const bool live = cur >= 0 && cur < P.nodes;
-        if (!__builtin_amdgcn_ballot_w64(live)) break;
-        if (live && cur >= tbase && cur < tbase + kTile) okbits |= 1u << (cur - tbase);
-        const int nx = parent_of(live ? cur : 0);
-        cur = live ? nx : -1;
-      }
-    }
+    const uint32_t okbits =
+        is_draft ? ancestor_bits(parr, P.nodes, node, tbase)
+                 : prefix_bits(len - tbase, ph[0], ph[1], P.phys_pages);
     // Stage K and V rows; rows that are not valid tokens may hold any bits
     // (NaN included): their weight is zero, so their V row must be zero.
 #pragma unroll
@@ -652,84 +755,12 @@ __global__ __launch_bounds__(64 * W, 2) void tree_split_kernel(TreeParams P) {
       *reinterpret_cast<uint4*>(vs + tl * VP + lcol) =
           (rowok >> s) & 1u ? vreg[s] : make_uint4(0, 0, 0, 0);
     }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    wave_lds_sync();
     // The rows are in LDS: the next tile's loads go out now.
     if (idx + 1 < nmine) issue(idx + 1, next_ids);
-
-    // ---- S^T = K Q^T, two independent MFMA chains over the k-steps ----
-    f32x16 sc0, sc1;
-#pragma unroll
-    for (int j = 0; j < 16; ++j) sc0[j] = sc1[j] = 0.f;
-#pragma unroll
-    for (int s = 0; s < KS; s += 2) {
-      const uint4 k0 = *reinterpret_cast<const uint4*>(ks + lr * KP + 16 * s + 8 * g);
-      const uint4 k1 = *reinterpret_cast<const uint4*>(ks + lr * KP + 16 * (s + 1) + 8 * g);
-      sc0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_f16x8(k0), as_f16x8(qB[s]), sc0, 0, 0, 0);
-      sc1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_f16x8(k1), as_f16x8(qB[s + 1]), sc1, 0, 0,
-                                                   0);
-    }
-    // sc[j] holds token row 8*(j/4) + 4*g + j%4.
-    const uint32_t ob = okbits >> (4 * g);
-    float sv[16];
-    float tmax = kNegInf;
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const bool ok = (ob >> (8 * (j >> 2) + (j & 3))) & 1u;
-      sv[j] = ok ? (sc0[j] + sc1[j]) * P.scale_log2 : kNegInf;
-      tmax = __builtin_fmaxf(tmax, sv[j]);
-    }
-    tmax = __builtin_fmaxf(tmax, shfl_xor_f(tmax, 32));
-    const float mnew = __builtin_fmaxf(m, tmax);
-    if (__builtin_amdgcn_ballot_w64(mnew > m + kRescaleSlack)) {
-      const float alpha = fast_exp2(m - safe_max(mnew));
-      l *= alpha;
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-        for (int j = 0; j < 16; ++j) acc[dt][j] *= alpha;
-      m = mnew;
-    }
-    // P splits into an FP16 hi part -- p with the low 13 mantissa bits
-    // cleared, exact in FP16 for p in [2^-14, 2^8] -- and lo = p - hi (exact
-    // in FP32, then rounded to FP16), so P.V carries ~21 bits of P.
-    const float mb = safe_max(m);
-    f16x8 pb[2], pl[2];
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const float pr = fast_exp2(sv[j] - mb);
-      l += pr;
-      const float hi = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, pr) & 0xffffe000u);
-      pb[j >> 3][j & 7] = (_Float16)hi;
-      pl[j >> 3][j & 7] = (_Float16)(pr - hi);
-    }
-    // ---- O^T += V^T P^T; A operand tokens 16st + 8hf + 4g + k, dim lr ----
-    // The MFMAs go round the DT accumulators, so consecutive ones are
-    // independent.
-    f16x8 av[DT][2];
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-      for (int st = 0; st < 2; ++st) {
-        const f16x4 lo = lds_read_tr(vtr + (16 * st) * VP + 32 * dt);
-        const f16x4 hi = lds_read_tr(vtr + (16 * st + 8) * VP + 32 * dt);
-        av[dt][st] = f16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-      }
-#pragma unroll
-    for (int st = 0; st < 2; ++st)
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt)
-        acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[dt][st], pb[st], acc[dt], 0, 0, 0);
-#pragma unroll
-    for (int st = 0; st < 2; ++st)
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt)
-        acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[dt][st], pl[st], acc[dt], 0, 0, 0);
+    tile_math<D>(ks + lr * KP, vtr, qB, okbits, P.scale_log2, g, acc, m, l);
     // The staging area is rewritten by the next tile.
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    wave_lds_sync();
   };
 
   auto ids_of = [&](int idx, int (&ph)[2]) {
@@ -1191,374 +1222,6 @@ __global__ __launch_bounds__(kThreads, 2) void tree_rows_kernel(TreeParams P) {
   }
 }
 
-// Request-group variant for trees of one row tile per (request, KV head),
-// workspace path only.  The four waves take four requests of one KV head and
-// one prefix chunk.  When the requests' page ids over the chunk and their
-// chunk ends agree -- requests forked from one prefix -- the workgroup loads
-// each 32-token tile once into LDS for all four (the tree_rows_kernel
-// pipeline: D/64 16-byte chunks of K and of V per thread, two tiles ahead,
-// one barrier per tile), so a CU reads the shared prefix once per four
-// requests instead of once per request.  Otherwise, and for the draft part,
-// every wave walks its own request's tiles with its own loads (D/16 chunks
-// of K and of V per lane, one tile ahead) through its own LDS tile.  Masks,
-// softmax and the P.V product are those of tree_kernel.
-template <int D, bool VEC>
-__global__ __launch_bounds__(kThreads, 2) void tree_group_kernel(TreeParams P) {
-  constexpr int KS = D / 16;
-  constexpr int DT = D / 32;
-  constexpr int VP = v_pitch<D>();
-  constexpr int KP = D + 8;            // halves per staged K row
-  constexpr int CPR = D / 8;           // 16-byte chunks per token row
-  constexpr int CPT = kTile * CPR / kThreads;  // shared loads: chunks per thread
-  constexpr int CPL = kTile * CPR / 64;        // private loads: chunks per lane
-  static_assert(CPT * kThreads == kTile * CPR, "tile chunks split evenly");
-  constexpr int BUF = kTile * (KP + VP);       // halves per staged tile
-
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int g = lane >> 5;
-  const int lr = lane & 31;
-
-  const int ngroups = (P.batch + kWaves - 1) / kWaves;
-  const int kvh = blockIdx.x % P.hkv;
-  const int b0 = (blockIdx.x / P.hkv) % ngroups * kWaves;
-  const int part = blockIdx.x / (P.hkv * ngroups);
-  const int nact = min(kWaves, P.batch - b0);  // requests of this group
-  const bool active = wave < nact;
-  const int b = b0 + min(wave, nact - 1);
-  const bool drafts = part >= P.prefix_parts;
-  const int max_tokens = P.max_pages * BC_PAGE_SIZE;
-  const int pbeg = drafts ? 0 : part * P.chunk_tokens;
-
-  // Chunk ends of the group's requests (<= pbeg: no tiles in this chunk),
-  // and the page ids of the chunk compared against the first request's.
-  int pend[kWaves];
-#pragma unroll
-  for (int w = 0; w < kWaves; ++w) {
-    const int lw = max(0, min(P.lengths[b0 + min(w, nact - 1)], max_tokens));
-    pend[w] = drafts ? lw : min(pbeg + P.chunk_tokens, lw);
-  }
-  const int mylen = max(0, min(P.lengths[b], max_tokens));
-  // All of this goes out in one round: the page loads do not wait for the
-  // lengths, which only mask the comparison afterwards.
-  int mismatch = 0;
-  const int tp0 = pbeg / kTile;
-  int pg_b0[2] = {-1, -1}, pg_own[2] = {-1, -1};  // first tile's page ids
-  if (!drafts) {
-#pragma unroll
-    for (int q = 0; q < 2; ++q) {
-      const int pi = tp0 * (kTile / BC_PAGE_SIZE) + q;
-      if (pi < P.max_pages) {
-        pg_b0[q] = P.pages[(size_t)b0 * P.max_pages + pi];
-        pg_own[q] = P.pages[(size_t)b * P.max_pages + pi];
-      }
-    }
-    const int p0 = pbeg / BC_PAGE_SIZE;
-    const int np = (min(pbeg + P.chunk_tokens, max_tokens) - pbeg + BC_PAGE_SIZE - 1) /
-                   BC_PAGE_SIZE;
-    for (int j = threadIdx.x; j < np; j += kThreads) {
-      const int p = p0 + j;  // < max_pages: pbeg + 16 j < max_tokens
-      int id[kWaves];
-#pragma unroll
-      for (int w = 0; w < kWaves; ++w)
-        id[w] = P.pages[(size_t)(b0 + min(w, nact - 1)) * P.max_pages + p];
-#pragma unroll
-      for (int w = 1; w < kWaves; ++w)
-        if (w < nact && p * BC_PAGE_SIZE < pend[0] && id[w] != id[0]) mismatch = 1;
-    }
-  }
-  bool same_end = true;
-#pragma unroll
-  for (int w = 1; w < kWaves; ++w) same_end = same_end && (w >= nact || pend[w] == pend[0]);
-
-  const int r = lr;
-  const bool rvalid = active && r < P.rows;
-  const int node = rvalid ? r / P.group : 0;
-  const int h = kvh * P.group + (rvalid ? r % P.group : 0);
-
-  __shared__ int s_parent[kWaves][32];
-  __shared__ __attribute__((aligned(16))) _Float16 s_kv[kWaves * BUF];
-  __shared__ bool s_pok[2][2];
-
-  uint4 qB[KS];
-  {
-    const uint16_t* qp = P.dq + (((size_t)b * P.nodes + node) * P.hq + h) * D + 8 * g;
-#pragma unroll
-    for (int s = 0; s < KS; ++s) qB[s] = rvalid ? load8<VEC>(qp + 16 * s) : make_uint4(0, 0, 0, 0);
-  }
-  if (drafts && lane < 32)
-    s_parent[wave][lane] = P.parent[(size_t)b * P.nodes + min(lane, P.nodes - 1)];
-
-  const size_t tok_stride = (size_t)P.hkv * D;
-  // Token row `row` of prefix page `pg` (page 0 for an invalid page, staged
-  // as zero V and masked) at dims col..col+7 of this KV head.
-  auto prefix_off = [&](int pg, int row, int col) {
-    const bool pok = pg >= 0 && pg < P.phys_pages;
-    return (pok ? ((size_t)pg * BC_PAGE_SIZE + row % BC_PAGE_SIZE) * tok_stride : 0) +
-           (size_t)kvh * D + col;
-  };
-  // Shared-mode registers: two sets, tile i in set i & 1.  Tile 0's loads
-  // (from the first request's page ids) go out before the barrier that
-  // decides the mode; a private-mode workgroup drops them.
-  uint4 kreg[2][CPT], vreg[2][CPT];
-  int ph[2][2] = {{pg_b0[0], pg_b0[1]}, {-1, -1}};
-  auto load_shared = [&](int i, int set) {
-    const int (&pg)[2] = ph[set];
-#pragma unroll
-    for (int c = 0; c < CPT; ++c) {
-      const int chunk = (int)threadIdx.x + kThreads * c;
-      const int row = chunk / CPR, col = 8 * (chunk % CPR);
-      const size_t off = prefix_off(pg[row / BC_PAGE_SIZE], row, col);
-      kreg[set][c] = load8<VEC>(P.k + off);
-      vreg[set][c] = load8<VEC>(P.v + off);
-    }
-  };
-  if (!drafts) load_shared(0, 0);
-  // Also the barrier that publishes the parent arrays.
-  const int any_mismatch = __syncthreads_or(mismatch);
-  const bool shared = !drafts && same_end && !any_mismatch;
-  if (!drafts && pend[0] <= pbeg && same_end) return;  // no request has tiles here
-  f32x16 acc[DT];
-#pragma unroll
-  for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-    for (int j = 0; j < 16; ++j) acc[dt][j] = 0.f;
-  float m = kNegInf, l = 0.f;
-  const int trG = lane >> 4, trj = lane & 15;
-  const int vtr_off = (4 * (trG >> 1) + (trj >> 2)) * VP + 16 * (trG & 1) + 4 * (trj & 3);
-
-  // Valid-token mask of prefix tile tbase for the range [pbeg, pe).
-  auto prefix_bits = [&](int tbase, int pe, bool pok0, bool pok1) {
-    const int lo = min(max(pbeg - tbase, 0), kTile);
-    const int hi = min(max(pe - tbase, 0), kTile);
-    const uint32_t below_hi = hi >= kTile ? ~0u : (1u << hi) - 1u;
-    const uint32_t below_lo = lo >= kTile ? ~0u : (1u << lo) - 1u;
-    return (below_hi & ~below_lo) & ((pok0 ? 0x0000ffffu : 0u) | (pok1 ? 0xffff0000u : 0u));
-  };
-  // Ancestor mask of draft tile tbase for this lane's node.
-  auto draft_bits = [&](int tbase) {
-    uint32_t bits = 0;
-    int cur = node;
-    for (int steps = 0; steps < P.nodes && cur >= 0 && cur < P.nodes; ++steps) {
-      if (cur >= tbase && cur < tbase + kTile) bits |= 1u << (cur - tbase);
-      cur = s_parent[wave][cur];
-    }
-    return bits;
-  };
-
-  auto compute = [&](const _Float16* sk, uint32_t okbits) {
-    const _Float16* sv = sk + kTile * KP;
-    f32x16 sc;
-#pragma unroll
-    for (int j = 0; j < 16; ++j) sc[j] = 0.f;
-#pragma unroll
-    for (int s = 0; s < KS; ++s) {
-      const uint4 ka = *reinterpret_cast<const uint4*>(sk + lr * KP + 16 * s + 8 * g);
-      sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_f16x8(ka), as_f16x8(qB[s]), sc, 0, 0, 0);
-    }
-    const uint32_t ob = okbits >> (4 * g);
-    float svv[16];
-    float tmax = kNegInf;
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const bool ok = (ob >> (8 * (j >> 2) + (j & 3))) & 1u;
-      svv[j] = ok ? sc[j] * P.scale_log2 : kNegInf;
-      tmax = __builtin_fmaxf(tmax, svv[j]);
-    }
-    tmax = __builtin_fmaxf(tmax, shfl_xor_f(tmax, 32));
-    const float mnew = __builtin_fmaxf(m, tmax);
-    if (__builtin_amdgcn_ballot_w64(mnew > m + kRescaleSlack)) {
-      const float alpha = fast_exp2(m - safe_max(mnew));
-      l *= alpha;
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-        for (int j = 0; j < 16; ++j) acc[dt][j] *= alpha;
-      m = mnew;
-    }
-    const float mb = safe_max(m);
-    f16x8 pb[2], pl[2];
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const float pr = fast_exp2(svv[j] - mb);
-      l += pr;
-      const _Float16 hi = (_Float16)pr;
-      pb[j >> 3][j & 7] = hi;
-      pl[j >> 3][j & 7] = (_Float16)(pr - (float)hi);
-    }
-    const _Float16* vtr = sv + vtr_off;
-    f16x8 av[DT][2];
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-      for (int st = 0; st < 2; ++st) {
-        const f16x4 lo = lds_read_tr(vtr + (16 * st) * VP + 32 * dt);
-        const f16x4 hi = lds_read_tr(vtr + (16 * st + 8) * VP + 32 * dt);
-        av[dt][st] = f16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-      }
-#pragma unroll
-    for (int st = 0; st < 2; ++st)
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt)
-        acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[dt][st], pb[st], acc[dt], 0, 0, 0);
-#pragma unroll
-    for (int st = 0; st < 2; ++st)
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt)
-        acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[dt][st], pl[st], acc[dt], 0, 0, 0);
-  };
-
-  if (shared) {
-    // ---- one staged tile for every wave; range [pbeg, pend[0]) ----
-    const int pe = pend[0];
-    const int ntile = (pe - 1) / kTile - tp0 + 1;
-    auto page_ids = [&](int i, int (&pg)[2]) {
-#pragma unroll
-      for (int q = 0; q < 2; ++q) {
-        const int pi = (tp0 + i) * (kTile / BC_PAGE_SIZE) + q;
-        pg[q] = pi < P.max_pages ? P.pages[(size_t)b0 * P.max_pages + pi] : -1;
-      }
-    };
-    auto store_tile = [&](int i, int set) {
-      const int buf = i & 1;
-      const int tbase = (tp0 + i) * kTile;
-      _Float16* sk = s_kv + buf * BUF;
-      _Float16* sv = sk + kTile * KP;
-#pragma unroll
-      for (int c = 0; c < CPT; ++c) {
-        const int chunk = (int)threadIdx.x + kThreads * c;
-        const int row = chunk / CPR, col = 8 * (chunk % CPR);
-        const int pgq = ph[set][row / BC_PAGE_SIZE];
-        const int t = tbase + row;
-        const bool ok = pgq >= 0 && pgq < P.phys_pages && t >= pbeg && t < pe;
-        *reinterpret_cast<uint4*>(sk + row * KP + col) = kreg[set][c];
-        *reinterpret_cast<uint4*>(sv + row * VP + col) =
-            ok ? vreg[set][c] : make_uint4(0, 0, 0, 0);
-      }
-      if (threadIdx.x < 2) {
-        const int pgq = ph[set][threadIdx.x];
-        s_pok[buf][threadIdx.x] = pgq >= 0 && pgq < P.phys_pages;
-      }
-    };
-    if (ntile > 1) {
-      page_ids(1, ph[1]);
-      load_shared(1, 1);
-    }
-    store_tile(0, 0);
-    __syncthreads();
-    auto step = [&](int i, int set) {  // set = i & 1, a compile-time constant
-      if (i >= ntile) return;
-      if (i + 2 < ntile) {
-        page_ids(i + 2, ph[set]);
-        load_shared(i + 2, set);
-      }
-      if (active)
-        compute(s_kv + set * BUF,
-                prefix_bits((tp0 + i) * kTile, pe, s_pok[set][0], s_pok[set][1]));
-      if (i + 1 < ntile) store_tile(i + 1, set ^ 1);
-      __syncthreads();
-    };
-    for (int i = 0; i < ntile; i += 2) {
-      step(i, 0);
-      step(i + 1, 1);
-    }
-  } else if (active) {
-    // ---- this wave alone: its request's tiles through its own LDS tile ----
-    const int pe = drafts ? 0 : min(pbeg + P.chunk_tokens, mylen);
-    const int ntile_p = pe > pbeg ? (pe - 1) / kTile - tp0 + 1 : 0;
-    const int ntile = ntile_p + (drafts ? (P.nodes + kTile - 1) / kTile : 0);
-    _Float16* sk = s_kv + wave * BUF;
-    _Float16* sv = sk + kTile * KP;
-    uint4 preg[CPL], qreg[CPL];  // K and V chunks of the next tile
-    bool vok[CPL];
-    int pg[2] = {pg_own[0], pg_own[1]};
-    auto load_tile = [&](int i) {
-      const bool is_draft = i >= ntile_p;
-      const int tbase = is_draft ? (i - ntile_p) * kTile : (tp0 + i) * kTile;
-      if (!is_draft && i > 0) {
-#pragma unroll
-        for (int q = 0; q < 2; ++q) {
-          const int pi = (tp0 + i) * (kTile / BC_PAGE_SIZE) + q;
-          pg[q] = pi < P.max_pages ? P.pages[(size_t)b * P.max_pages + pi] : -1;
-        }
-      }
-#pragma unroll
-      for (int c = 0; c < CPL; ++c) {
-        const int chunk = lane + 64 * c;
-        const int row = chunk / CPR, col = 8 * (chunk % CPR);
-        if (!is_draft) {
-          const int pgq = pg[row / BC_PAGE_SIZE];
-          const int t = tbase + row;
-          const size_t off = prefix_off(pgq, row, col);
-          preg[c] = load8<VEC>(P.k + off);
-          qreg[c] = load8<VEC>(P.v + off);
-          vok[c] = pgq >= 0 && pgq < P.phys_pages && t >= pbeg && t < pe;
-        } else {
-          const int dn = tbase + row;
-          const size_t off =
-              (((size_t)b * P.nodes + min(dn, P.nodes - 1)) * P.hkv + kvh) * D + col;
-          preg[c] = load8<VEC>(P.dk + off);
-          qreg[c] = load8<VEC>(P.dv + off);
-          vok[c] = dn < P.nodes;
-        }
-      }
-    };
-    if (ntile > 0) load_tile(0);
-    for (int i = 0; i < ntile; ++i) {
-      const bool is_draft = i >= ntile_p;
-      const int tbase = is_draft ? (i - ntile_p) * kTile : (tp0 + i) * kTile;
-      const bool pok0 = pg[0] >= 0 && pg[0] < P.phys_pages;
-      const bool pok1 = pg[1] >= 0 && pg[1] < P.phys_pages;
-#pragma unroll
-      for (int c = 0; c < CPL; ++c) {
-        const int chunk = lane + 64 * c;
-        const int row = chunk / CPR, col = 8 * (chunk % CPR);
-        *reinterpret_cast<uint4*>(sk + row * KP + col) = preg[c];
-        *reinterpret_cast<uint4*>(sv + row * VP + col) = vok[c] ? qreg[c] : make_uint4(0, 0, 0, 0);
-      }
-      if (i + 1 < ntile) load_tile(i + 1);
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      compute(sk, is_draft ? draft_bits(tbase) : prefix_bits(tbase, pe, pok0, pok1));
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    }
-  }
-  // This wave's rows: nothing to write when its request has no tokens in
-  // this prefix chunk (the merge does not read that slot).
-  const int own_end = drafts ? 0 : min(pbeg + P.chunk_tokens, mylen);
-  if (!rvalid || (!drafts && own_end <= pbeg)) return;
-  l += shfl_xor_f(l, 32);
-
-  if (drafts && mylen == 0) {
-    float* dst = P.out + (((size_t)b * P.nodes + node) * P.hq + h) * D;
-    const float inv = 1.f / l;
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-      for (int jq = 0; jq < 4; ++jq)
-        store4f<VEC>(dst + 32 * dt + 8 * jq + 4 * g, acc[dt][4 * jq] * inv,
-                     acc[dt][4 * jq + 1] * inv, acc[dt][4 * jq + 2] * inv,
-                     acc[dt][4 * jq + 3] * inv);
-  } else {
-    const size_t slot = slot_index(P, b, node, h, drafts ? P.prefix_parts : part);
-    float* dst = P.part_acc + slot * D;
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-      for (int jq = 0; jq < 4; ++jq)
-        *reinterpret_cast<float4*>(dst + 32 * dt + 8 * jq + 4 * g) =
-            make_float4(acc[dt][4 * jq], acc[dt][4 * jq + 1], acc[dt][4 * jq + 2],
-                        acc[dt][4 * jq + 3]);
-    if (g == 0) {
-      P.part_ml[2 * slot] = m;
-      P.part_ml[2 * slot + 1] = l;
-    }
-  }
-}
-
 // Combines the prefix chunks and the draft part of every (b, node, h): one
 // wave per output row, lane p reads slot p's (max, sum), the weights are
 // formed once and every lane accumulates its dims with independent loads.
@@ -1634,8 +1297,8 @@ __global__ __launch_bounds__(256) void merge_tree_kernel(TreeParams P) {
 bool tree_args_ok(const bc_shape& s, const bc_tree_inputs& in, int nodes) {
   return s.batch >= 1 && s.query_heads >= 1 && s.kv_heads >= 1 &&
          s.query_heads % s.kv_heads == 0 && (s.dim == 64 || s.dim == 128) &&
-         s.max_pages >= 1 && nodes >= 1 && nodes <= BC_MAX_TREE_NODES &&
-         in.prefix.k && in.prefix.v && in.prefix.pages && in.prefix.lengths &&
+         s.max_pages >= 1 && s.physical_pages >= 1 && nodes >= 1 &&
+         nodes <= BC_MAX_TREE_NODES && in.prefix.k && in.prefix.v && in.prefix.pages && in.prefix.lengths &&
          in.draft_q && in.draft_k && in.draft_v && in.parent && in.output;
 }
 
@@ -1693,14 +1356,6 @@ int row_units(int row_tiles, bool rows_kernel) {
   return rows_kernel ? (row_tiles + kWaves - 1) / kWaves : row_tiles;
 }
 
-// bc_tree_verify_shared_ws runs tree_group_kernel for one row tile per
-// (request, KV head) and at least two full groups of four requests; at four
-// requests or fewer it measured slower than tree_kernel even on one shared
-// prefix (4 x 2048: 15.2 against 14.6 us).
-bool group_kernel_for(int batch, int row_tiles) {
-  return row_tiles == 1 && batch >= 2 * kWaves;
-}
-
 // Prefix tokens per chunk for `want` chunks: multiples of 32, at least
 // `floor`, and at most 63 chunks (the merge reads one partial per lane).
 int chunk_for(int max_tokens, long long want, int floor = 128) {
@@ -1713,46 +1368,21 @@ int chunk_for(int max_tokens, long long want, int floor = 128) {
   return chunk;
 }
 
-void tree_chunking(const bc_shape& s, int nodes, bool grouped, int* chunk_tokens,
-                   int* parts) {
+// Prefix chunks of the workspace path of tree_rows_kernel (large trees): it
+// walks its tiles in series, so it takes two workgroups per CU (two fit).
+void tree_chunking(const bc_shape& s, int nodes, int* chunk_tokens, int* parts) {
   const int group = s.query_heads / s.kv_heads;
   const int row_tiles = (nodes * group + 31) / 32;
   const int cus = bch::device_cus();
   const int max_tokens = s.max_pages * BC_PAGE_SIZE;
-  int chunk;
-  if (grouped) {
-    // tree_group_kernel walks its tiles in series: two workgroups per CU,
-    // unless the chunk floor leaves a partial second round, which then
-    // shrinks to one round (8 x 2053 tokens: 288 workgroups 18.4 us, 224
-    // workgroups 17.7 us).  Its floor is three tiles (8 x 1024 tokens: 14.3
-    // against 14.9 us with four).
-    const long long units = (long long)s.kv_heads * ((s.batch + kWaves - 1) / kWaves);
-    chunk = chunk_for(max_tokens, 2LL * cus / units - 1, 96);
-    const long long wgs = ((max_tokens + chunk - 1) / chunk + 1) * units;
-    if (wgs > cus && wgs < 2LL * cus - units)
-      chunk = chunk_for(max_tokens, cus / units - 1, 96);
-  } else {
-    const bool rows = rows_kernel_for(s.batch, s.kv_heads, row_tiles, true, cus);
-    const long long units = (long long)s.batch * s.kv_heads * row_units(row_tiles, rows);
-    // tree_rows_kernel walks its tiles in series, so it takes two workgroups
-    // per CU (two fit); tree_kernel's four waves split the tiles, one per CU.
-    long long want = (rows ? 2LL * cus : cus) / units - 1;
-    // With units in (cus/3, cus/2] the rule above gives tree_kernel a single
-    // chunk, which leaves half or more of the CUs idle while each workgroup
-    // walks the whole prefix; two chunks plus the draft part keep every
-    // workgroup resident (two per CU) and measured 25-26 us against 35 us at
-    // 12 and 16 requests of a 2048-token prefix.  More units than that
-    // measured slower with two.
-    if (!rows && want < 2 && 2LL * units <= cus) want = 2;
-    chunk = chunk_for(max_tokens, want);
-  }
+  const long long units = (long long)s.batch * s.kv_heads * row_units(row_tiles, true);
+  const int chunk = chunk_for(max_tokens, 2LL * cus / units - 1);
   *chunk_tokens = chunk;
   *parts = (max_tokens + chunk - 1) / chunk;
 }
 
-size_t tree_workspace(const bc_shape& s, int nodes, bool grouped, int* chunk_tokens,
-                      int* parts) {
-  tree_chunking(s, nodes, grouped, chunk_tokens, parts);
+size_t tree_workspace(const bc_shape& s, int nodes, int* chunk_tokens, int* parts) {
+  tree_chunking(s, nodes, chunk_tokens, parts);
   if (*parts <= 1) return 0;
   const size_t slots = (size_t)s.batch * nodes * s.query_heads * (*parts + 1);
   const size_t acc = (slots * s.dim * sizeof(float) + 255) & ~(size_t)255;
@@ -1760,33 +1390,26 @@ size_t tree_workspace(const bc_shape& s, int nodes, bool grouped, int* chunk_tok
 }
 
 template <int D, bool VEC>
-void launch_tree_kernel(const TreeParams& P, bool group_kernel, bool rows_kernel, dim3 grid,
-                        hipStream_t st) {
-  if (group_kernel)
-    tree_group_kernel<D, VEC><<<grid, kThreads, 0, st>>>(P);
-  else if (rows_kernel)
+void launch_tree_kernel(const TreeParams& P, bool rows_kernel, dim3 grid, hipStream_t st) {
+  if (rows_kernel)
     tree_rows_kernel<D, VEC><<<grid, kThreads, 0, st>>>(P);
-  else
-    tree_kernel<D, VEC><<<grid, kThreads, 0, st>>>(P);
+  else  // only unaligned tensors get here: the split kernel takes the rest
+    tree_kernel<D, false><<<grid, kThreads, 0, st>>>(P);
 }
 
 // vec: every FP16 tensor and the output are 16-byte aligned (16-byte loads
 // and stores); otherwise the kernels move single halves and floats.
-hipError_t launch_tree(TreeParams& P, int dim, int parts, bool grouped, bool vec,
-                       hipStream_t st) {
+hipError_t launch_tree(TreeParams& P, int dim, int parts, bool vec, hipStream_t st) {
   const bool rows_kernel = rows_kernel_for(P.batch, P.hkv, P.row_tiles, P.part_acc != nullptr,
                                            bch::device_cus());
-  const bool group_kernel = grouped && P.part_acc;
   const dim3 grid(
-      group_kernel
-          ? (unsigned)((size_t)parts * P.hkv * ((P.batch + kWaves - 1) / kWaves))
-          : (unsigned)((size_t)parts * P.batch * P.hkv * row_units(P.row_tiles, rows_kernel)));
+      (unsigned)((size_t)parts * P.batch * P.hkv * row_units(P.row_tiles, rows_kernel)));
   if (dim == 64) {
-    if (vec) launch_tree_kernel<64, true>(P, group_kernel, rows_kernel, grid, st);
-    else launch_tree_kernel<64, false>(P, group_kernel, rows_kernel, grid, st);
+    if (vec) launch_tree_kernel<64, true>(P, rows_kernel, grid, st);
+    else launch_tree_kernel<64, false>(P, rows_kernel, grid, st);
   } else {
-    if (vec) launch_tree_kernel<128, true>(P, group_kernel, rows_kernel, grid, st);
-    else launch_tree_kernel<128, false>(P, group_kernel, rows_kernel, grid, st);
+    if (vec) launch_tree_kernel<128, true>(P, rows_kernel, grid, st);
+    else launch_tree_kernel<128, false>(P, rows_kernel, grid, st);
   }
   hipError_t err = hipGetLastError();
   if (err != hipSuccess || !P.part_acc) return err;
@@ -1806,18 +1429,22 @@ bool tree_ptrs_aligned(const bc_tree_inputs& in) {
 // ---- tree_split_kernel: plan, workspace and launch ----
 
 struct SplitPlan {
-  int parts;  // workgroups per (request, KV head, row tile), <= 64
-  int tiles;  // 32-token tiles per workgroup (prefix then draft tiles)
+  int parts;  // workgroups per (request group, KV head, row tile), <= 64
+  int tiles;  // 32-token tiles per workgroup and request (draft then prefix tiles)
   int waves;  // waves per workgroup: 4 or 8
 };
 
 // Parts per unit and tiles per part for `cus` compute units, sized from the
-// page table's capacity (lengths stay on the device).  Eight-wave workgroups
-// (one per CU) with about one workgroup per CU over all units, every wave
-// with a tile; where that leaves CUs idle (few units: one request, short
-// prefixes), four-wave workgroups with one tile per wave, which spread the
-// tiles over twice the workgroups and merge in fewer LDS steps (one request
-// x 2048 tokens: 10.4 against 11.8 us; eight requests: 17.0 against 15.6).
+// page table's capacity (lengths stay on the device).  A CU holds one
+// eight-wave or two four-wave workgroups (LDS), so both shapes offer eight
+// wave slots per CU: eight-wave workgroups take about cus/units parts, four-
+// wave ones about 2*cus/units.  The plan with more waves that have a tile
+// wins (12 requests x 2048 tokens, 96 units: four waves x 5 parts 20.2 us
+// against eight waves x 2 parts 20.8 and four waves x 2 parts 24.5); at about
+// equal counts, the one spread over more CUs (one request x 2048 tokens:
+// four waves x 17 parts, 10.4 against 11.8 us), else eight waves, which
+// merge more tiles in LDS (8 and 16 requests), or run single-pass (24 and 32
+// requests: one part, 28.6 against 31.7 us with two).
 SplitPlan split_plan(const bc_shape& s, int nodes, int cus) {
   const int group = s.query_heads / s.kv_heads;
   const int row_tiles = (nodes * group + 31) / 32;
@@ -1835,8 +1462,16 @@ SplitPlan split_plan(const bc_shape& s, int nodes, int cus) {
   };
   const long long u = units > 0 ? units : 1;
   const SplitPlan eight = plan_for(8, cus / u);
-  if (eight.parts == 1 || eight.parts * u >= cus) return eight;
-  return plan_for(4, cus / u);
+  const SplitPlan four = plan_for(4, 2LL * cus / u);
+  // Waves with at least one tile, and CUs with a workgroup.
+  auto busy = [&](const SplitPlan& p) {
+    return u * std::min<long long>((long long)p.parts * p.waves, max_tiles);
+  };
+  auto spread = [&](const SplitPlan& p) { return std::min<long long>(u * p.parts, cus); };
+  const long long b8 = busy(eight), b4 = busy(four);
+  if (10 * b4 > 11 * b8) return four;
+  if (eight.parts > 1 && 10 * b4 >= 9 * b8 && spread(four) > spread(eight)) return four;
+  return eight;
 }
 
 // Workspace of tree_split_kernel: P.parts (acc; max, sum) slots per output row.
@@ -1848,8 +1483,9 @@ size_t split_workspace(const bc_shape& s, int nodes, const SplitPlan& plan, size
 }
 
 template <int D>
-void launch_split_kernel(const TreeParams& P, int waves, dim3 grid, hipStream_t st) {
-  if (waves == 4)
+void launch_split_kernel(const TreeParams& P, const SplitPlan& plan, dim3 grid,
+                         hipStream_t st) {
+  if (plan.waves == 4)
     tree_split_kernel<D, 4><<<grid, 256, 0, st>>>(P);
   else
     tree_split_kernel<D, 8><<<grid, 512, 0, st>>>(P);
@@ -1864,8 +1500,8 @@ hipError_t launch_split(TreeParams& P, int dim, const SplitPlan& plan, void* wor
     P.part_ml = reinterpret_cast<float*>(static_cast<char*>(workspace) + acc_bytes);
   }
   const dim3 grid((unsigned)((size_t)plan.parts * P.batch * P.hkv * P.row_tiles));
-  if (dim == 64) launch_split_kernel<64>(P, plan.waves, grid, st);
-  else launch_split_kernel<128>(P, plan.waves, grid, st);
+  if (dim == 64) launch_split_kernel<64>(P, plan, grid, st);
+  else launch_split_kernel<128>(P, plan, grid, st);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess || plan.parts < 2) return err;
   const size_t rows = (size_t)P.batch * P.nodes * P.hq;
@@ -1889,7 +1525,7 @@ extern "C" int bc_tree_verify(bc_shape s, bc_tree_inputs in, int nodes,
         (s.max_pages * BC_PAGE_SIZE + kTile - 1) / kTile + (nodes + kTile - 1) / kTile;
     return launch_split(P, s.dim, SplitPlan{1, max_tiles, 8}, nullptr, 0, st);
   }
-  return launch_tree(P, s.dim, 1, false, vec, st);
+  return launch_tree(P, s.dim, 1, vec, st);
 }
 
 namespace {
@@ -1897,12 +1533,8 @@ namespace {
 bool tree_shape_ok(const bc_shape& s, int nodes) {
   return s.batch >= 1 && s.query_heads >= 1 && s.kv_heads >= 1 &&
          s.query_heads % s.kv_heads == 0 && (s.dim == 64 || s.dim == 128) &&
-         s.max_pages >= 1 && nodes >= 1 && nodes <= BC_MAX_TREE_NODES;
-}
-
-bool grouped_for(const bc_shape& s, int nodes) {
-  const int row_tiles = (nodes * (s.query_heads / s.kv_heads) + 31) / 32;
-  return group_kernel_for(s.batch, row_tiles);
+         s.max_pages >= 1 && s.physical_pages >= 1 && nodes >= 1 &&
+         nodes <= BC_MAX_TREE_NODES;
 }
 
 bool split_for(const bc_shape& s, int nodes) {
@@ -1910,24 +1542,24 @@ bool split_for(const bc_shape& s, int nodes) {
   return !rows_kernel_for(s.batch, s.kv_heads, row_tiles, true, bch::device_cus());
 }
 
-size_t ws_size(const bc_shape& s, int nodes, bool grouped) {
-  if (!grouped && split_for(s, nodes)) {
+size_t ws_size(const bc_shape& s, int nodes) {
+  if (split_for(s, nodes)) {
     size_t a = 0;
     return split_workspace(s, nodes, split_plan(s, nodes, bch::device_cus()), &a);
   }
   int chunk = 0, parts = 0;
-  return tree_workspace(s, nodes, grouped, &chunk, &parts);
+  return tree_workspace(s, nodes, &chunk, &parts);
 }
 
-int tree_ws_call(bc_shape s, bc_tree_inputs in, int nodes, bool grouped, void* workspace,
+int tree_ws_call(bc_shape s, bc_tree_inputs in, int nodes, void* workspace,
                  size_t workspace_bytes, bc_stream_t stream) {
   if (!tree_args_ok(s, in, nodes)) return BC_ERROR_INVALID_VALUE;
   const bool vec = tree_ptrs_aligned(in);
   // Tensors that are not 16-byte aligned take the element-wise single pass.
   if (!vec) return bc_tree_verify(s, in, nodes, stream);
   const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  if (!grouped && split_for(s, nodes)) {
-    SplitPlan plan = split_plan(s, nodes, bch::device_cus());
+  if (split_for(s, nodes)) {
+    const SplitPlan plan = split_plan(s, nodes, bch::device_cus());
     size_t acc = 0;
     const size_t need = split_workspace(s, nodes, plan, &acc);
     if (!workspace || need == 0 || workspace_bytes < need || !aligned16(workspace))
@@ -1936,7 +1568,7 @@ int tree_ws_call(bc_shape s, bc_tree_inputs in, int nodes, bool grouped, void* w
     return launch_split(P, s.dim, plan, workspace, acc, st);
   }
   int chunk = 0, parts = 0;
-  const size_t need = tree_workspace(s, nodes, grouped, &chunk, &parts);
+  const size_t need = tree_workspace(s, nodes, &chunk, &parts);
   if (!workspace || need == 0 || workspace_bytes < need || !aligned16(workspace))
     return bc_tree_verify(s, in, nodes, stream);
   TreeParams P = make_params(s, in, nodes);
@@ -1946,31 +1578,18 @@ int tree_ws_call(bc_shape s, bc_tree_inputs in, int nodes, bool grouped, void* w
   const size_t acc = (slots * s.dim * sizeof(float) + 255) & ~(size_t)255;
   P.part_acc = static_cast<float*>(workspace);
   P.part_ml = reinterpret_cast<float*>(static_cast<char*>(workspace) + acc);
-  return launch_tree(P, s.dim, parts + 1, grouped, true, st);
+  return launch_tree(P, s.dim, parts + 1, true, st);
 }
 
 }  // namespace
 
 extern "C" size_t bc_tree_verify_workspace_size(bc_shape s, int nodes) {
   if (!tree_shape_ok(s, nodes)) return 0;
-  return ws_size(s, nodes, false);
+  return ws_size(s, nodes);
 }
 
 extern "C" int bc_tree_verify_ws(bc_shape s, bc_tree_inputs in, int nodes,
                                  void* workspace, size_t workspace_bytes,
                                  bc_stream_t stream) {
-  return tree_ws_call(s, in, nodes, false, workspace, workspace_bytes, stream);
-}
-
-extern "C" size_t bc_tree_verify_shared_workspace_size(bc_shape s, int nodes) {
-  if (!tree_shape_ok(s, nodes)) return 0;
-  return ws_size(s, nodes, grouped_for(s, nodes));
-}
-
-extern "C" int bc_tree_verify_shared_ws(bc_shape s, bc_tree_inputs in, int nodes,
-                                        void* workspace, size_t workspace_bytes,
-                                        bc_stream_t stream) {
-  if (!tree_shape_ok(s, nodes)) return BC_ERROR_INVALID_VALUE;
-  return tree_ws_call(s, in, nodes, grouped_for(s, nodes), workspace, workspace_bytes,
-                      stream);
+  return tree_ws_call(s, in, nodes, workspace, workspace_bytes, stream);
 }

@@ -27,9 +27,7 @@ BC_MAX_TREE_NODES = 256
 # Every entry point include/branchcraft.h declares.
 EXPORTED = (
     "bc_decode", "bc_auto_splits", "bc_tree_verify",
-    "bc_tree_verify_workspace_size", "bc_tree_verify_ws",
-    "bc_tree_verify_shared_workspace_size", "bc_tree_verify_shared_ws", "bc_commit_path",
-    "bc_commit_paths", "bc_copy_pages", "bc_packed_decode", "bc_packed_decode_workspace_size",
+    "bc_tree_verify_workspace_size", "bc_tree_verify_ws", "bc_commit_path", "bc_commit_paths", "bc_copy_pages", "bc_packed_decode", "bc_packed_decode_workspace_size",
     "bc_packed_decode_ws", "bc_packed_decode_noalloc", "bc_version",
 )
 
@@ -73,13 +71,8 @@ def load(path: str | Path | None = None) -> ctypes.CDLL:
     lib.bc_tree_verify.restype = c_int
     lib.bc_tree_verify_workspace_size.argtypes = [Shape, c_int]
     lib.bc_tree_verify_workspace_size.restype = c_size_t
-    lib.bc_tree_verify_shared_workspace_size.argtypes = [Shape, c_int]
-    lib.bc_tree_verify_shared_workspace_size.restype = c_size_t
     lib.bc_tree_verify_ws.argtypes = [Shape, TreeInputs, c_int, c_void_p, c_size_t, c_void_p]
     lib.bc_tree_verify_ws.restype = c_int
-    lib.bc_tree_verify_shared_ws.argtypes = [Shape, TreeInputs, c_int, c_void_p, c_size_t,
-                                             c_void_p]
-    lib.bc_tree_verify_shared_ws.restype = c_int
     lib.bc_commit_path.argtypes = [Shape, c_void_p, c_void_p, c_void_p, c_void_p,
                                    c_void_p, c_void_p, c_void_p, c_int, c_int, c_int,
                                    c_void_p]

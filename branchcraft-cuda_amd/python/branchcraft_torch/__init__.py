@@ -4,10 +4,9 @@ Importing this module loads ``_C.so`` (built in-tree by
 ``branchcraft-cuda_amd/build.py``) which registers ``torch.ops.branchcraft``
 with the reference's schemas (bindings/torch_ops.cpp:144-148 of
 Haaziq386/branchcraft-cuda) plus ``paged_decode`` (the reference's C++
-``branchcraft::decode``), ``copy_pages_``, ``commit_paths_`` and
-``tree_verify_shared``.  There is no CPU or
-Python fallback: a missing extension raises ImportError, and the ops have
-only a GPU implementation.
+``branchcraft::decode``), ``copy_pages_`` and ``commit_paths_``.  There is
+no CPU or Python fallback: a missing extension raises ImportError, and the
+ops have only a GPU implementation.
 
 FakeTensor implementations follow python/branchcraft_torch/__init__.py:18-31
 of the reference so that ``torch.compile`` can trace the ops.
@@ -27,11 +26,6 @@ LIBRARY_PATH = str(_library)
 
 @torch.library.register_fake("branchcraft::tree_verify")
 def _fake_tree_verify(q, prefix_k, prefix_v, pages, lengths, draft_k, draft_v, parent):
-    return q.new_empty(q.shape, dtype=torch.float32)
-
-
-@torch.library.register_fake("branchcraft::tree_verify_shared")
-def _fake_tree_verify_shared(q, prefix_k, prefix_v, pages, lengths, draft_k, draft_v, parent):
     return q.new_empty(q.shape, dtype=torch.float32)
 
 
@@ -66,14 +60,6 @@ def tree_verify(q, prefix_k, prefix_v, pages, lengths, draft_k, draft_v, parent)
     """FP32 [batch, node, query head, dim] outputs; every node attends to its
     request's paged prefix and its own ancestor chain (itself included)."""
     return torch.ops.branchcraft.tree_verify(
-        q, prefix_k, prefix_v, pages, lengths, draft_k, draft_v, parent)
-
-
-def tree_verify_shared(q, prefix_k, prefix_v, pages, lengths, draft_k, draft_v, parent):
-    """tree_verify for requests forked from one prefix (no reference
-    counterpart): the same outputs, faster when the requests' page tables
-    agree and slower when they do not."""
-    return torch.ops.branchcraft.tree_verify_shared(
         q, prefix_k, prefix_v, pages, lengths, draft_k, draft_v, parent)
 
 
@@ -115,5 +101,5 @@ def commit_paths_(cache_k, cache_v, draft_k, draft_v, requests, path_nodes, dest
         cache_k, cache_v, draft_k, draft_v, requests, path_nodes, dest_pages, dest_slots)
 
 
-__all__ = ["tree_verify", "tree_verify_shared", "packed_decode_out", "paged_decode",
+__all__ = ["tree_verify", "packed_decode_out", "paged_decode",
            "commit_path_", "copy_pages_", "commit_paths_", "LIBRARY_PATH"]

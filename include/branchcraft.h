@@ -113,7 +113,8 @@ int bc_auto_splits(bc_shape shape, int max_length, int cu_count);
  * (src/tree_attention.cu:93-105).  Runs without scratch: one workgroup
  * per (request, KV head, row tile) streams the whole prefix.  Tensors that
  * are not 16-byte aligned are read and written element by element.
- * Rejects: batch/Hq/Hkv < 1, Hq % Hkv != 0, dim not 64/128, max_pages < 1,
+ * Rejects: batch/Hq/Hkv < 1, Hq % Hkv != 0, dim not 64/128, max_pages or
+ * physical_pages < 1 (page ids outside the pool read page 0, masked),
  * nodes outside [1, BC_MAX_TREE_NODES], a null K/V, page table, lengths,
  * draft tensor, parent array or output. */
 int bc_tree_verify(bc_shape shape, bc_tree_inputs in, int nodes,
@@ -131,22 +132,6 @@ size_t bc_tree_verify_workspace_size(bc_shape shape, int nodes);
 int bc_tree_verify_ws(bc_shape shape, bc_tree_inputs in, int nodes,
                       void* workspace, size_t workspace_bytes,
                       bc_stream_t stream);
-
-/* No counterpart in the reference; for callers whose requests were forked
- * from one prefix (PagedTreeCache.fork, python/branchcraft_torch/
- * transaction.py:73-80, copies the source's page table).  bc_tree_verify_ws
- * for trees whose query rows fit one row tile per (request, KV head), with
- * eight or more requests: each workgroup takes four consecutive requests of
- * one KV head and one prefix chunk, and loads each tile once for all four
- * when their page ids and chunk ends agree (otherwise every request walks
- * its own pages, slower than bc_tree_verify_ws but with the same results).
- * Other shapes run exactly as bc_tree_verify_ws.  `workspace` holds at
- * least bc_tree_verify_shared_workspace_size bytes, with the same fallbacks
- * as bc_tree_verify_ws. */
-size_t bc_tree_verify_shared_workspace_size(bc_shape shape, int nodes);
-int bc_tree_verify_shared_ws(bc_shape shape, bc_tree_inputs in, int nodes,
-                             void* workspace, size_t workspace_bytes,
-                             bc_stream_t stream);
 
 /* Copy accepted draft K/V rows into physical cache slots:
  * cache[dest_pages[i], dest_slots[i]] <- draft[request, path_nodes[i]] for

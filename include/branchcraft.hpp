@@ -125,17 +125,6 @@ inline hipError_t tree_verify(Shape shape, TreeInputs in, int nodes, void* works
                                        workspace_bytes, detail::stream(stream)));
 }
 
-// Requests forked from one prefix (bc_tree_verify_shared_ws).
-inline size_t tree_verify_shared_workspace_size(Shape shape, int nodes) {
-  return bc_tree_verify_shared_workspace_size(shape, nodes);
-}
-
-inline hipError_t tree_verify_shared(Shape shape, TreeInputs in, int nodes, void* workspace,
-                                     size_t workspace_bytes, hipStream_t stream = nullptr) {
-  return detail::err(bc_tree_verify_shared_ws(shape, detail::to_c(in), nodes, workspace,
-                                              workspace_bytes, detail::stream(stream)));
-}
-
 // Reference: include/branchcraft.hpp:61-65.
 inline hipError_t commit_path(Shape shape, const half* draft_k, const half* draft_v,
                               half* cache_k, half* cache_v, const int* path_nodes,

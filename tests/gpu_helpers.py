@@ -50,10 +50,10 @@ def decode(q, k, v, pages, lengths, splits, *, keep=False, out=None):
     return o.cpu().numpy()
 
 
-def tree(k, v, pages, lengths, dq, dk, dv, parent, *, workspace=True, ws_offset=0,
-         shared=False):
-    """ws_offset shifts the workspace pointer by that many bytes (the size
-    passed stays the required one); shared calls bc_tree_verify_shared_ws."""
+def tree(k, v, pages, lengths, dq, dk, dv, parent, *, workspace=True, ws_offset=0):
+    """bc_tree_verify_ws (workspace) or bc_tree_verify.  ws_offset shifts the
+    workspace pointer by that many bytes (the size passed stays the required
+    one)."""
     b, n, hq, d = dq.shape
     P, _, hkv, _ = k.shape
     tk, tv = dev(k), dev(v)
@@ -68,12 +68,10 @@ def tree(k, v, pages, lengths, dq, dk, dv, parent, *, workspace=True, ws_offset=
                           tpar.data_ptr(), o.data_ptr())
     L = lib()
     if workspace:
-        size_fn, call = ((L.bc_tree_verify_shared_workspace_size, L.bc_tree_verify_shared_ws)
-                         if shared else (L.bc_tree_verify_workspace_size, L.bc_tree_verify_ws))
-        nbytes = size_fn(shape, n)
+        nbytes = L.bc_tree_verify_workspace_size(shape, n)
         ws = torch.empty(max(1, nbytes + ws_offset), device="cuda", dtype=torch.uint8)
-        check(call(shape, ins, n, ws.data_ptr() + ws_offset, nbytes, stream()),
-              "bc_tree_verify_shared_ws" if shared else "bc_tree_verify_ws")
+        check(L.bc_tree_verify_ws(shape, ins, n, ws.data_ptr() + ws_offset, nbytes, stream()),
+              "bc_tree_verify_ws")
     else:
         check(L.bc_tree_verify(shape, ins, n, stream()), "bc_tree_verify")
     torch.cuda.synchronize()

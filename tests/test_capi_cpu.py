@@ -85,9 +85,7 @@ def test_tree_rejects_node_count(nodes):
     lib = capi.load()
     assert lib.bc_tree_verify(_shape(), _tree_inputs(), nodes, None) == INVALID
     assert lib.bc_tree_verify_ws(_shape(), _tree_inputs(), nodes, None, 0, None) == INVALID
-    assert lib.bc_tree_verify_shared_ws(_shape(), _tree_inputs(), nodes, None, 0,
-                                        None) == INVALID
-    assert lib.bc_tree_verify_shared_workspace_size(_shape(), nodes) == 0
+    assert lib.bc_tree_verify_workspace_size(_shape(), nodes) == 0
 
 
 @pytest.mark.parametrize("field", ["draft_q", "draft_k", "draft_v", "parent", "output"])
@@ -225,20 +223,13 @@ def test_workspace_sizes():
     c3 = capi.Shape(8, 32, 8, 128, 129, 160)
     assert lib.bc_tree_verify_workspace_size(c3, 7) > 0
     assert lib.bc_tree_verify_workspace_size(c3, 0) == 0
-    # Trees split the prefix while (request, KV head, row tile) units number at
-    # most half the CUs (two chunks plus the draft part per unit), and run in
-    # one pass beyond that.
-    for batch, split in ((12, True), (16, True), (17, False), (20, False), (32, False)):
+    # Trees split the prefix while splitting gives more waves a tile (eight
+    # wave slots per CU): 17 requests (136 units) take three four-wave parts,
+    # 24 and 32 requests one eight-wave pass.
+    for batch, split in ((12, True), (16, True), (17, True), (20, True), (24, False),
+                         (32, False)):
         size = lib.bc_tree_verify_workspace_size(capi.Shape(batch, 32, 8, 128, 129, 160), 7)
         assert (size > 0) == split, batch
-    # The shared-prefix entry point chunks finer for eight or more requests of
-    # one row tile (four requests per workgroup), and sizes like
-    # bc_tree_verify_ws otherwise.
-    shared = lib.bc_tree_verify_shared_workspace_size
-    assert shared(c3, 7) > lib.bc_tree_verify_workspace_size(c3, 7)
-    for shape, nodes in ((capi.Shape(7, 32, 8, 128, 129, 160), 7), (c3, 9),
-                         (capi.Shape(8, 32, 8, 128, 129, 160), 256)):
-        assert shared(shape, nodes) == lib.bc_tree_verify_workspace_size(shape, nodes)
 
 
 def test_torch_ops_register_reference_schemas():

@@ -3,7 +3,7 @@
 
 * tree_verify: ancestor mask against the oracle (D=64/128, lengths [23, 0]),
   torch.compile(inductor) equality and opcheck schema/FakeTensor checks;
-* tree_verify_shared (added): forked requests against the oracle and tree_verify;
+  and forked requests (one page table, a copied last page, a shorter request);
 * packed_decode_out: HND and NHD-transposed caches and the 5-D
   [P, 2, 16, Hkv, D] layout, output aliasing, and HIP-graph capture replayed
   several times with eager work in between, every replay checked;
@@ -54,10 +54,10 @@ def test_tree_mask_compile_and_opcheck(dim):
                           test_utils=("test_schema", "test_faketensor"))
 
 
-def test_tree_verify_shared_op_on_forked_requests():
-    """tree_verify_shared (bc_tree_verify_shared_ws): ten requests forked
-    from one page table, one with a copied last page and one shorter, match
-    the oracle and tree_verify; schema and FakeTensor checks as above."""
+def test_tree_verify_op_on_forked_requests():
+    """Ten requests forked from one page table (as PagedTreeCache.fork
+    leaves them), one with a copied last page and one shorter, against the
+    oracle."""
     torch.manual_seed(8)
     batch, nodes, hq, hkv, dim = 10, 7, 8, 2, 128
     q = torch.randn(batch, nodes, hq, dim, device="cuda", dtype=torch.float16)
@@ -72,14 +72,11 @@ def test_tree_verify_shared_op_on_forked_requests():
     draft_v = torch.randn_like(draft_k)
     parent = torch.tensor([[-1, 0, 0, 1, 1, 2, 2]] * batch, device="cuda", dtype=torch.int32)
     args = (q, prefix_k, prefix_v, pages, lengths, draft_k, draft_v, parent)
-    actual = bc.tree_verify_shared(*args)
+    actual = bc.tree_verify(*args)
     assert actual.dtype == torch.float32 and actual.shape == q.shape
     qn, pk, pv, pg, ln, dk, dv, par = (a.cpu().numpy() for a in args)
     expected = oracle_c.tree(pk, pv, pg, ln, qn, dk, dv, par, threads=8)
-    G.gate(actual.cpu().numpy(), expected, 3e-4, "tree_verify_shared op")
-    torch.testing.assert_close(actual, bc.tree_verify(*args), atol=2e-6, rtol=0)
-    torch.library.opcheck(torch.ops.branchcraft.tree_verify_shared, args,
-                          test_utils=("test_schema", "test_faketensor"))
+    G.gate(actual.cpu().numpy(), expected, 3e-4, "tree_verify op, forked requests")
 
 
 def _packed_case(layout, dim=64):

@@ -19,12 +19,12 @@ pytestmark = pytest.mark.gpu
 
 
 def _check(fix, oracle, atol=3e-4, what=""):
-    """bc_tree_verify, bc_tree_verify_ws and bc_tree_verify_shared_ws."""
+    """bc_tree_verify and bc_tree_verify_ws."""
     k, v, pages, lengths, dq, dk, dv, par = fix
     expected = oracle.tree(k, v, pages, lengths, dq, dk, dv, par, threads=16)
-    for ws, shared in ((False, False), (True, False), (True, True)):
-        out = G.tree(k, v, pages, lengths, dq, dk, dv, par, workspace=ws, shared=shared)
-        G.gate(out, expected, atol, f"{what} workspace={ws} shared={shared}")
+    for ws in (False, True):
+        out = G.tree(k, v, pages, lengths, dq, dk, dv, par, workspace=ws)
+        G.gate(out, expected, atol, f"{what} workspace={ws}")
     return expected
 
 
@@ -102,7 +102,7 @@ def test_garbage_past_prefix_is_ignored(oracle):
     v[last, 37 % 16:] = np.float16(np.inf)
     for ws in (False, True):
         G.gate(G.tree(k, v, pages, lengths, dq, dk, dv, par, workspace=ws), expected, 3e-4,
-               "garbage slots")
+               f"garbage slots workspace={ws}")
 
 
 def test_mid_batch_splits_the_prefix(oracle):
@@ -175,16 +175,13 @@ def _group_fixture(rng, lengths, share, nodes=7, hq=32, hkv=8, d=128, cow_last=(
     dict(lengths=[517] * 8, share=[-1] + [0] * 7, nodes=8, hq=8, hkv=2, d=64),
     # group 1: 32 nodes fill the row tile and the draft tile
     dict(lengths=[290] * 8, share=[-1] + [0] * 7, nodes=32, hq=8, hkv=8),
-    # fewer than eight requests: bc_tree_verify_shared_ws runs as bc_tree_verify_ws
+    # five requests, two page tables
     dict(lengths=[613, 613, 400, 613, 613], share=[-1, 0, 0, -1, 3]),
 ])
 def test_per_request_page_tables(case, oracle):
     """Requests whose page tables share some pages and not others, end at
     different lengths, hold a copied last page or are empty, with and
-    without a workspace.  With eight or more requests of one row tile,
-    bc_tree_verify_shared_ws runs tree_group_kernel: four requests per
-    workgroup, each prefix chunk loaded once for all of them where their
-    page ids and chunk ends agree, else every wave on its own pages."""
+    without a workspace."""
     rng = np.random.default_rng(len(case["lengths"]) * 7 + sum(case["lengths"]))
     fix = _group_fixture(rng, **case)
     k, v, pages, lengths, dq, dk, dv, par = fix
@@ -215,7 +212,7 @@ def test_malformed_parent_arrays_end_the_walk(oracle):
     and one cycle through all nodes.  Every kernel's walk is bounded by N
     steps and stops outside [0, N), so each row attends to the set of nodes
     its walk reaches, as the oracle's walk (which stops at the first repeat)
-    does; all three entry points run, the shared one on tree_group_kernel."""
+    does; both entry points run."""
     rng = np.random.default_rng(61)
     fix = list(oracle_np.tree_fixture(rng, 8, 300, 7, sigma=1.0, parents="random"))
     par = fix[7].copy()
