@@ -604,7 +604,7 @@ __device__ __forceinline__ void wave_lds_sync() {
 // merge through LDS; with one part per unit (no workspace) wave 0 writes the
 // output, otherwise every part with tiles writes an FP32 partial per row,
 // slot (row, part), and merge_split_kernel combines them.
-template <int D, int W>
+template <int D, int W, int RQ>
 __global__ __launch_bounds__(64 * W, 2) void tree_split_kernel(TreeParams P) {
   constexpr int KS = D / 16;      // MFMA k-steps; also load instructions per tile
   constexpr int DT = D / 32;      // 32-row output tiles over the head dimension
@@ -614,18 +614,26 @@ __global__ __launch_bounds__(64 * W, 2) void tree_split_kernel(TreeParams P) {
   constexpr int RPI = 64 / LPR;   // token rows per load instruction
   static_assert(RPI * KS == kTile, "KS whole-row loads cover a tile");
   constexpr int STAGE = kTile * (KP + VP);  // halves per wave
+  constexpr int LN = W / RQ;      // waves per request
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int g = lane >> 5;   // lane half
   const int lr = lane & 31;  // tile column (query row) / token slot
 
+  // RQ requests per workgroup: wave w serves request RQ*group + w/LN and
+  // takes every LN-th tile from w%LN, so the RQ requests walk the same
+  // tiles at the same time (their shared pages then meet in the CU's L1).
+  const int rq = wave / LN;
+  const int ln = wave % LN;
   const int zdim = P.hkv * P.row_tiles;
-  const int units = zdim * P.batch;
+  const int units = zdim * ((P.batch + RQ - 1) / RQ);
   const int unit = blockIdx.x % units;  // (KV head, row tile) in the low bits
   const int part = blockIdx.x / units;
   const int z = unit % zdim;
-  const int b = unit / zdim;
+  const int b0 = (unit / zdim) * RQ;
+  const bool present = b0 + rq < P.batch;  // uniform per wave
+  const int b = present ? b0 + rq : b0;    // absent waves read request b0, unused
   const int kvh = z / P.row_tiles;
   const int rt = z % P.row_tiles;
   const int T = P.tiles_per_part;
@@ -639,25 +647,26 @@ __global__ __launch_bounds__(64 * W, 2) void tree_split_kernel(TreeParams P) {
   // the wave's tiles or the prefix are unused).
   const int ntd = (P.nodes + kTile - 1) / kTile;  // draft tiles come first
   auto load_ids = [&](int chunk) {
-    const int it = tbeg + wave + W * (chunk * 32 + (lane >> 1));
+    const int it = tbeg + ln + LN * (chunk * 32 + (lane >> 1));
     const int pg = (it - ntd) * (kTile / BC_PAGE_SIZE) + (lane & 1);
     return it < tbeg + T && pg >= 0 && pg < P.max_pages ? P.pages[(size_t)b * P.max_pages + pg]
                                                          : -1;
   };
   // Tile 0's ids as scalar loads: with the length they are all the first
   // K/V loads wait for.
-  const int pg0 = (tbeg + wave - ntd) * (kTile / BC_PAGE_SIZE);
+  const int pg0 = (tbeg + ln - ntd) * (kTile / BC_PAGE_SIZE);
   int cur[2] = {pg0 >= 0 && pg0 < P.max_pages ? P.pages[(size_t)b * P.max_pages + pg0] : -1,
                 pg0 >= 0 && pg0 + 1 < P.max_pages ? P.pages[(size_t)b * P.max_pages + pg0 + 1]
                                                   : -1};
   int idv = load_ids(0);
   int idv_next = -1;
-  if (T > 32 * W) idv_next = load_ids(1);
+  if (T > 32 * LN) idv_next = load_ids(1);
   const int len = max(0, min(P.lengths[b], P.max_pages * BC_PAGE_SIZE));
   const int ntp = (len + kTile - 1) / kTile;
   const int ntot = ntd + ntp;
   const int tend = min(tbeg + T, ntot);
-  const int nmine = tend > tbeg + wave ? (tend - tbeg - wave + W - 1) / W : 0;
+  const int nmine =
+      present && tend > tbeg + ln ? (tend - tbeg - ln + LN - 1) / LN : 0;
 
   const int r = rt * 32 + lr;
   const bool rvalid = r < P.rows;
@@ -705,7 +714,7 @@ __global__ __launch_bounds__(64 * W, 2) void tree_split_kernel(TreeParams P) {
   // outside the pool read page 0 and rows past the length read their page's
   // rows (all in bounds); both are masked.
   auto issue = [&](int idx, const int (&ph)[2]) {
-    const int it = tbeg + wave + W * idx - ntd;  // prefix tile index when >= 0
+    const int it = tbeg + ln + LN * idx - ntd;  // prefix tile index when >= 0
     rowok = 0;
     if (it >= 0) {
       const int tb = it * kTile;
@@ -737,7 +746,7 @@ __global__ __launch_bounds__(64 * W, 2) void tree_split_kernel(TreeParams P) {
   };
 
   auto process = [&](int idx, const int (&ph)[2], const int (&next_ids)[2]) {
-    const int it = tbeg + wave + W * idx;
+    const int it = tbeg + ln + LN * idx;
     const bool is_draft = it < ntd;
     const int tbase = (is_draft ? it : it - ntd) * kTile;
     // Valid token rows of the tile as a bit mask (bit i = token tbase + i):
@@ -766,7 +775,7 @@ __global__ __launch_bounds__(64 * W, 2) void tree_split_kernel(TreeParams P) {
   auto ids_of = [&](int idx, int (&ph)[2]) {
     if ((idx & 31) == 0 && idx > 0) {  // uniform: move to the next chunk of ids
       idv = idv_next;
-      if (T > 32 * W * ((idx >> 5) + 1)) idv_next = load_ids((idx >> 5) + 1);
+      if (T > 32 * LN * ((idx >> 5) + 1)) idv_next = load_ids((idx >> 5) + 1);
     }
     ph[0] = __builtin_amdgcn_readlane(idv, 2 * (idx & 31));
     ph[1] = __builtin_amdgcn_readlane(idv, 2 * (idx & 31) + 1);
@@ -798,9 +807,10 @@ __global__ __launch_bounds__(64 * W, 2) void tree_split_kernel(TreeParams P) {
   }
   l += shfl_xor_f(l, 32);  // both lane halves share m
 
-  // ---- merge the W waves through LDS in one step ----
+  // ---- merge each request's LN waves through LDS in one step ----
   // Every wave stores its state; after one barrier each thread combines the
-  // W states of its share of the tile (row mrow, DPT dims) and writes it.
+  // LN states of its request's share of the tile (row mrow, DPT dims) and
+  // writes it.
   constexpr int XP = D + 4;  // padded rows: a float4 access spreads over banks
   static_assert(W * STAGE * 2 >= W * 32 * XP * 4, "merge buffer fits");
   float* xacc = reinterpret_cast<float*>(s_stage);  // [W][32 rows][XP]
@@ -821,17 +831,19 @@ __global__ __launch_bounds__(64 * W, 2) void tree_split_kernel(TreeParams P) {
     }
   }
   __syncthreads();
-  constexpr int TPR = 2 * W;    // threads per row
+  constexpr int TPR = 2 * LN;   // threads per row
   constexpr int DPT = D / TPR;  // dims per thread
   static_assert(DPT % 4 == 0, "float4 steps");
-  const int mrow = threadIdx.x / TPR;
-  const int md0 = (threadIdx.x % TPR) * DPT;
+  const int t = threadIdx.x % (64 * LN);  // the request's waves hold its rows
+  const int mrow = t / TPR;
+  const int md0 = (t % TPR) * DPT;
   const int rr = rt * 32 + mrow;
-  if (rr >= P.rows) return;
-  float mw[W], mm = kNegInf;
+  if (!present || rr >= P.rows) return;
+  const int w0 = rq * LN;
+  float mw[LN], mm = kNegInf;
 #pragma unroll
-  for (int w = 0; w < W; ++w) {
-    mw[w] = s_ml[w][mrow][0];
+  for (int w = 0; w < LN; ++w) {
+    mw[w] = s_ml[w0 + w][mrow][0];
     mm = __builtin_fmaxf(mm, mw[w]);
   }
   const float ms = safe_max(mm);  // all waves empty: every weight is 0
@@ -839,10 +851,10 @@ __global__ __launch_bounds__(64 * W, 2) void tree_split_kernel(TreeParams P) {
 #pragma unroll
   for (int j = 0; j < DPT; ++j) o[j] = 0.f;
 #pragma unroll
-  for (int w = 0; w < W; ++w) {
+  for (int w = 0; w < LN; ++w) {
     const float wt = fast_exp2(mw[w] - ms);  // 0 for a wave without tiles
-    ll += wt * s_ml[w][mrow][1];
-    const float* src = xacc + ((size_t)w * 32 + mrow) * XP + md0;
+    ll += wt * s_ml[w0 + w][mrow][1];
+    const float* src = xacc + ((size_t)(w0 + w) * 32 + mrow) * XP + md0;
 #pragma unroll
     for (int j = 0; j < DPT; j += 4) {
       const float4 v4 = *reinterpret_cast<const float4*>(src + j);
@@ -1432,7 +1444,27 @@ struct SplitPlan {
   int parts;  // workgroups per (request group, KV head, row tile), <= 64
   int tiles;  // 32-token tiles per workgroup and request (draft then prefix tiles)
   int waves;  // waves per workgroup: 4 or 8
+  int rq = 1;  // requests per workgroup (waves / rq per request)
 };
+
+// A single pass of more (request, KV head, row tile) units than CUs runs
+// its eight-wave workgroups (one per CU) in rounds.  Two requests per
+// workgroup, four waves each on the same tiles, halve the workgroups and
+// double each wave's tiles, so they pay where they at least halve the
+// rounds; requests that share pages then also share them in the CU's L1.
+// Measured against one request per workgroup (32 / 8 heads, D = 128, 7
+// nodes, shared prefix): 33 x 2048 tokens 48.9 -> 45.3 us, 40 x 1024 31.6
+// -> 28.2, 64 x 1024 32.4 -> 30.1, 128 x 512 46.3 -> 39.2; 96 x 512 (three
+// rounds against two) 35.5 -> 37.9 and 32 x 2048 (one round) 27.9 -> 45.7,
+// so neither of those pairs.
+SplitPlan pair_requests(int batch, long long units, SplitPlan p, int cus) {
+  if (p.parts != 1 || p.waves != 8 || batch < 2) return p;
+  const long long per_request = units / batch;  // KV heads x row tiles
+  const long long rounds1 = (units + cus - 1) / cus;
+  const long long rounds2 = ((batch + 1) / 2 * per_request + cus - 1) / cus;
+  if (2 * rounds2 <= rounds1) p.rq = 2;
+  return p;
+}
 
 // Parts per unit and tiles per part for `cus` compute units, sized from the
 // page table's capacity (lengths stay on the device).  A CU holds one
@@ -1444,7 +1476,8 @@ struct SplitPlan {
 // equal counts, the one spread over more CUs (one request x 2048 tokens:
 // four waves x 17 parts, 10.4 against 11.8 us), else eight waves, which
 // merge more tiles in LDS (8 and 16 requests), or run single-pass (24 and 32
-// requests: one part, 28.6 against 31.7 us with two).
+// requests: one part, 28.6 against 31.7 us with two); see pair_requests for
+// single passes of more units than CUs.
 SplitPlan split_plan(const bc_shape& s, int nodes, int cus) {
   const int group = s.query_heads / s.kv_heads;
   const int row_tiles = (nodes * group + 31) / 32;
@@ -1471,7 +1504,7 @@ SplitPlan split_plan(const bc_shape& s, int nodes, int cus) {
   const long long b8 = busy(eight), b4 = busy(four);
   if (10 * b4 > 11 * b8) return four;
   if (eight.parts > 1 && 10 * b4 >= 9 * b8 && spread(four) > spread(eight)) return four;
-  return eight;
+  return pair_requests(s.batch, u, eight, cus);
 }
 
 // Workspace of tree_split_kernel: P.parts (acc; max, sum) slots per output row.
@@ -1486,9 +1519,11 @@ template <int D>
 void launch_split_kernel(const TreeParams& P, const SplitPlan& plan, dim3 grid,
                          hipStream_t st) {
   if (plan.waves == 4)
-    tree_split_kernel<D, 4><<<grid, 256, 0, st>>>(P);
+    tree_split_kernel<D, 4, 1><<<grid, 256, 0, st>>>(P);
+  else if (plan.rq == 2)
+    tree_split_kernel<D, 8, 2><<<grid, 512, 0, st>>>(P);
   else
-    tree_split_kernel<D, 8><<<grid, 512, 0, st>>>(P);
+    tree_split_kernel<D, 8, 1><<<grid, 512, 0, st>>>(P);
 }
 
 hipError_t launch_split(TreeParams& P, int dim, const SplitPlan& plan, void* workspace,
@@ -1499,7 +1534,8 @@ hipError_t launch_split(TreeParams& P, int dim, const SplitPlan& plan, void* wor
     P.part_acc = static_cast<float*>(workspace);
     P.part_ml = reinterpret_cast<float*>(static_cast<char*>(workspace) + acc_bytes);
   }
-  const dim3 grid((unsigned)((size_t)plan.parts * P.batch * P.hkv * P.row_tiles));
+  const size_t groups = ((size_t)P.batch + plan.rq - 1) / plan.rq;
+  const dim3 grid((unsigned)((size_t)plan.parts * groups * P.hkv * P.row_tiles));
   if (dim == 64) launch_split_kernel<64>(P, plan, grid, st);
   else launch_split_kernel<128>(P, plan, grid, st);
   hipError_t err = hipGetLastError();
@@ -1520,10 +1556,13 @@ extern "C" int bc_tree_verify(bc_shape s, bc_tree_inputs in, int nodes,
   P.prefix_parts = 0;
   const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const bool vec = tree_ptrs_aligned(in);
-  if (vec && !rows_kernel_for(P.batch, P.hkv, P.row_tiles, false, bch::device_cus())) {
+  const int cus = bch::device_cus();
+  if (vec && !rows_kernel_for(P.batch, P.hkv, P.row_tiles, false, cus)) {
     const int max_tiles =
         (s.max_pages * BC_PAGE_SIZE + kTile - 1) / kTile + (nodes + kTile - 1) / kTile;
-    return launch_split(P, s.dim, SplitPlan{1, max_tiles, 8}, nullptr, 0, st);
+    const long long units = (long long)P.batch * P.hkv * P.row_tiles;
+    return launch_split(P, s.dim, pair_requests(P.batch, units, SplitPlan{1, max_tiles, 8}, cus),
+                        nullptr, 0, st);
   }
   return launch_tree(P, s.dim, 1, vec, st);
 }

@@ -191,6 +191,27 @@ def test_per_request_page_tables(case, oracle):
     _check(fix, oracle, atol=3e-4, what=str(case))
 
 
+@pytest.mark.parametrize("case", [
+    # 40 requests on one page table: 320 (request, KV head) units
+    dict(lengths=[700] * 40, share=[-1] + [0] * 39),
+    # 33 requests (the last workgroup holds one), mixed tables, empty requests
+    dict(lengths=[611, 0, 870, 402, 333, 777, 128, 640, 95, 513, 513] * 3,
+         share=[j + 11 * (i // 11) if j >= 0 else -1
+                for i, j in enumerate([-1, -1, -1, 2, -1, 4, -1, 6, -1, 8, 9] * 3)],
+         cow_last=(10, 21)),
+    # D = 64 at 8 KV heads
+    dict(lengths=[300] * 40, share=[-1] + [0] * 39, hq=32, hkv=8, d=64),
+])
+def test_large_batches_pair_requests(case, oracle):
+    """Batches with more (request, KV head) units than CUs run in one pass
+    with two requests per workgroup (four waves each, walking the same
+    tiles), with and without a workspace; 33 requests leave the last
+    workgroup one."""
+    rng = np.random.default_rng(len(case["lengths"]) * 11 + sum(case["lengths"]))
+    fix = _group_fixture(rng, **case)
+    _check(fix, oracle, atol=3e-4, what=f"B={len(case['lengths'])}")
+
+
 def test_misaligned_workspace_runs_single_pass():
     """A workspace that is not 16-byte aligned is ignored: the call gives the
     same bits as bc_tree_verify."""
