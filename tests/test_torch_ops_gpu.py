@@ -3,7 +3,8 @@
 
 * tree_verify: ancestor mask against the oracle (D=64/128, lengths [23, 0]),
   torch.compile(inductor) equality and opcheck schema/FakeTensor checks;
-  and forked requests (one page table, a copied last page, a shorter request);
+  forked requests (one page table, a copied last page, a shorter request) and
+  HIP-graph capture of the split kernel and its merge, replayed several times;
 * packed_decode_out: HND and NHD-transposed caches and the 5-D
   [P, 2, 16, Hkv, D] layout, output aliasing, and HIP-graph capture replayed
   several times with eager work in between, every replay checked;
@@ -77,6 +78,43 @@ def test_tree_verify_op_on_forked_requests():
     qn, pk, pv, pg, ln, dk, dv, par = (a.cpu().numpy() for a in args)
     expected = oracle_c.tree(pk, pv, pg, ln, qn, dk, dv, par, threads=8)
     G.gate(actual.cpu().numpy(), expected, 3e-4, "tree_verify op, forked requests")
+
+
+def test_tree_verify_graph_replay():
+    """tree_verify captured in a HIP graph: the split kernel and its merge
+    (8 requests x 700 tokens take several parts per (request, KV head)) with
+    the output and workspace from the graph's pool, replayed with eager work
+    in between; every replay equals the eager call bit for bit, which
+    matches the oracle."""
+    torch.manual_seed(21)
+    batch, nodes, hq, hkv, dim = 8, 7, 32, 8, 128
+    q = torch.randn(batch, nodes, hq, dim, device="cuda", dtype=torch.float16)
+    prefix_k = torch.randn(48, 16, hkv, dim, device="cuda", dtype=torch.float16)
+    prefix_v = torch.randn_like(prefix_k)
+    pages = torch.randperm(48, device="cuda").to(torch.int32)[:44].repeat(batch, 1)
+    lengths = torch.full((batch,), 700, device="cuda", dtype=torch.int32)
+    draft_k = torch.randn(batch, nodes, hkv, dim, device="cuda", dtype=torch.float16)
+    draft_v = torch.randn_like(draft_k)
+    parent = torch.tensor([[-1, 0, 0, 1, 1, 2, 2]] * batch, device="cuda", dtype=torch.int32)
+    args = (q, prefix_k, prefix_v, pages, lengths, draft_k, draft_v, parent)
+    shape = capi.Shape(batch, hq, hkv, dim, pages.shape[1], prefix_k.shape[0])
+    assert G.lib().bc_tree_verify_workspace_size(shape, nodes) > 0  # split + merge
+    eager = bc.tree_verify(*args)
+    qn, pk, pv, pg, ln, dk, dv, par = (a.cpu().numpy() for a in args)
+    expected = oracle_c.tree(pk, pv, pg, ln, qn, dk, dv, par, threads=8)
+    G.gate(eager.cpu().numpy(), expected, 3e-4, "tree_verify eager")
+    bc.tree_verify(*args)  # warm the allocator outside capture
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        captured = bc.tree_verify(*args)
+    for i in range(4):
+        captured.fill_(float("nan"))
+        junk = torch.randn(1024, 1024, device="cuda").sum()  # unrelated eager work
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(captured, eager), f"replay {i}"
+        del junk
 
 
 def _packed_case(layout, dim=64):
