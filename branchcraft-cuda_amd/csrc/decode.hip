@@ -726,7 +726,7 @@ extern "C" int bc_auto_splits(bc_shape s, int max_length, int cu_count) {
   // splits == 1 runs one workgroup per (sequence, head block) with the pages
   // split kSlices ways inside it and no merge kernel: the faster choice while
   // every slice is short (contexts up to 768 tokens, or 1024 for batches
-  // that fill most of the CUs) and those workgroups fit the CUs at once.  Otherwise split decode runs flat page ranges: (splits -
+  // that fill half the CUs or more) and those workgroups fit the CUs at once.  Otherwise split decode runs flat page ranges: (splits -
   // 1) * batch + 1 of them, rounded down to whole waves of one workgroup per
   // CU.  Pick the smallest split count that reaches a full wave, so that no CU
   // idles: at batch 64 two splits would leave 65 of 128 ranges (55 % of HBM
@@ -743,11 +743,12 @@ extern "C" int bc_auto_splits(bc_shape s, int max_length, int cu_count) {
   const int group = s.query_heads / s.kv_heads;
   const long long zdim = (long long)s.kv_heads * ((group + kHeadCols - 1) / kHeadCols);
   // Unsplit up to 768 tokens; up to 1024 only where the batch's workgroups
-  // already fill more than half the CUs (1024 tokens, 32/8 heads: one
-  // sequence 12.3 us unsplit against 9.7 us split; 32 sequences 23.5 us
-  // unsplit against 24.9 us at the best split count).
+  // already fill half the CUs or more (1024 tokens, 32/8 heads, same box:
+  // one sequence 12.3 us unsplit against 9.7 us split, 8 sequences 14.4
+  // against 12.7, 12 sequences 16.0 against 16.0, 16 sequences 17.0 against
+  // 18.0, 32 sequences 23.5 against 24.9 at the best split count).
   const long long wgs = (long long)s.batch * zdim;
-  if (wgs <= cus && (max_length <= 768 || (max_length <= 1024 && 2 * wgs > cus))) return 1;
+  if (wgs <= cus && (max_length <= 768 || (max_length <= 1024 && 2 * wgs >= cus))) return 1;
   const int per_wave = cus / zgroups_of(s);
   if (per_wave <= 1) return 1;
   if (s.batch >= per_wave) return s.batch <= 2 * per_wave ? 2 : 1;

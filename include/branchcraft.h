@@ -190,9 +190,10 @@ int bc_packed_decode(bc_shape shape, const bc_half* q, const bc_half* packed_kv,
 
 /* Bytes of workspace bc_packed_decode_ws needs for this shape.  0 when
  * bc_auto_splits, given the table's capacity (max_pages * 16 tokens), keeps
- * the shape unsplit: a table of at most 1024 tokens whose (sequence, head
- * block) workgroups fit the CUs, or a batch above two waves of flat ranges
- * (256 sequences at 8 KV heads on 256 CUs).  Such calls run unsplit, with no
+ * the shape unsplit: a table under 512 tokens; one of at most 768 tokens
+ * whose (sequence, head block) workgroups fit the CUs, or of at most 1024
+ * tokens whose workgroups fill half the CUs or more; or a batch above two
+ * waves of flat ranges (256 sequences at 8 KV heads on 256 CUs).  Such calls run unsplit, with no
  * merge, whatever workspace is passed. */
 size_t bc_packed_decode_workspace_size(bc_shape shape);
 

@@ -184,7 +184,8 @@ def test_auto_splits_policy():
     assert lib.bc_auto_splits(_shape(batch=1), 512, 256) == 1
     assert lib.bc_auto_splits(_shape(batch=1), 768, 256) == 1
     assert lib.bc_auto_splits(_shape(batch=1), 769, 256) > 1
-    assert lib.bc_auto_splits(_shape(batch=16), 1024, 256) > 1
+    assert lib.bc_auto_splits(_shape(batch=12), 1024, 256) > 1
+    assert lib.bc_auto_splits(_shape(batch=16), 1024, 256) == 1
     assert lib.bc_auto_splits(_shape(batch=32), 1024, 256) == 1
     assert lib.bc_auto_splits(_shape(batch=33), 1024, 256) > 1
     assert lib.bc_auto_splits(_shape(batch=1), 1025, 256) > 1
@@ -208,8 +209,8 @@ def test_workspace_sizes():
     c5 = capi.Shape(64, 32, 8, 128, 256, 20000)
     assert lib.bc_packed_decode_workspace_size(c5) > 0
     # Page tables of at most 768 tokens (1024 for batches whose (sequence,
-    # head block) workgroups fill more than half the CUs) whose workgroups
-    # fit the CUs run unsplit: no workspace.
+    # head block) workgroups fill half the CUs or more) whose workgroups fit
+    # the CUs run unsplit: no workspace.
     assert lib.bc_packed_decode_workspace_size(capi.Shape(4, 32, 8, 128, 8, 64)) == 0
     assert lib.bc_packed_decode_workspace_size(capi.Shape(4, 32, 8, 128, 48, 64)) == 0
     assert lib.bc_packed_decode_workspace_size(capi.Shape(4, 32, 8, 128, 49, 64)) > 0
