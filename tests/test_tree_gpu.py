@@ -201,6 +201,8 @@ def test_per_request_page_tables(case, oracle):
          cow_last=(10, 21)),
     # D = 64 at 8 KV heads
     dict(lengths=[300] * 40, share=[-1] + [0] * 39, hq=32, hkv=8, d=64),
+    # 16 nodes: two row tiles per (request, KV head), 1,024 units
+    dict(lengths=[300] * 64, share=[-1] + [0] * 63, nodes=16),
 ])
 def test_large_batches_pair_requests(case, oracle):
     """Batches with more (request, KV head) units than CUs run in one pass
