@@ -523,17 +523,21 @@ __device__ __forceinline__ void tile_math(const _Float16* kr, const _Float16* vt
     sc1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_f16x8(k1), as_f16x8(qB[s + 1]), sc1, 0, 0,
                                                  0);
   }
-  // sc[j] holds token row 8*(j/4) + 4*g + j%4.
-  const uint32_t ob = okbits >> (4 * g);
+  // sc[j] holds token row 8*(j/4) + 4*g + j%4.  Scores stay unscaled here;
+  // the scale enters the running max once and the exp2 argument as an FMA.
   float sv[16];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) sv[j] = sc0[j] + sc1[j];
+  if (__builtin_amdgcn_ballot_w64(okbits != ~0u)) {  // masked tokens in the tile
+    const uint32_t ob = okbits >> (4 * g);
+#pragma unroll
+    for (int j = 0; j < 16; ++j)
+      sv[j] = (ob >> (8 * (j >> 2) + (j & 3))) & 1u ? sv[j] : kNegInf;
+  }
   float tmax = kNegInf;
 #pragma unroll
-  for (int j = 0; j < 16; ++j) {
-    const bool ok = (ob >> (8 * (j >> 2) + (j & 3))) & 1u;
-    sv[j] = ok ? (sc0[j] + sc1[j]) * scale_log2 : kNegInf;
-    tmax = __builtin_fmaxf(tmax, sv[j]);
-  }
-  tmax = __builtin_fmaxf(tmax, shfl_xor_f(tmax, 32));
+  for (int j = 0; j < 16; ++j) tmax = __builtin_fmaxf(tmax, sv[j]);
+  tmax = __builtin_fmaxf(tmax, shfl_xor_f(tmax, 32)) * scale_log2;
   const float mnew = __builtin_fmaxf(m, tmax);
   if (__builtin_amdgcn_ballot_w64(mnew > m + kRescaleSlack)) {
     const float alpha = fast_exp2(m - safe_max(mnew));
@@ -551,7 +555,7 @@ __device__ __forceinline__ void tile_math(const _Float16* kr, const _Float16* vt
   f16x8 pb[2], pl[2];
 #pragma unroll
   for (int j = 0; j < 16; ++j) {
-    const float pr = fast_exp2(sv[j] - mb);
+    const float pr = fast_exp2(__builtin_fmaf(sv[j], scale_log2, -mb));
     l += pr;
     const float hi = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, pr) & 0xffffe000u);
     pb[j >> 3][j & 7] = (_Float16)hi;
