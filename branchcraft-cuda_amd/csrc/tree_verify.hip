@@ -705,6 +705,7 @@ __global__ __launch_bounds__(64 * W, 2) void tree_split_kernel(TreeParams P) {
 
   uint4 kreg[KS], vreg[KS];
   uint32_t rowok = 0;  // bit s: this lane's row of load s is a valid token
+  constexpr uint32_t kAllRows = (1u << KS) - 1;
   // Byte offset of this lane's 16 bytes in whole-row load j of a page (j <
   // KS/2 loads per page: token row j*RPI + lrow, dims lcol .. +8); a prefix
   // tile's loads are then a uniform page base plus these offsets.
@@ -765,8 +766,13 @@ __global__ __launch_bounds__(64 * W, 2) void tree_split_kernel(TreeParams P) {
     for (int s = 0; s < KS; ++s) {
       const int tl = s * RPI + lrow;
       *reinterpret_cast<uint4*>(ks + tl * KP + lcol) = kreg[s];
-      *reinterpret_cast<uint4*>(vs + tl * VP + lcol) =
-          (rowok >> s) & 1u ? vreg[s] : make_uint4(0, 0, 0, 0);
+      *reinterpret_cast<uint4*>(vs + tl * VP + lcol) = vreg[s];
+    }
+    if (__builtin_amdgcn_ballot_w64(rowok != kAllRows)) {  // rows past the data: zero V
+#pragma unroll
+      for (int s = 0; s < KS; ++s)
+        if (!((rowok >> s) & 1u))
+          *reinterpret_cast<uint4*>(vs + (s * RPI + lrow) * VP + lcol) = make_uint4(0, 0, 0, 0);
     }
     wave_lds_sync();
     // The rows are in LDS: the next tile's loads go out now.
