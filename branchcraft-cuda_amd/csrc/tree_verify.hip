@@ -499,7 +499,7 @@ __device__ __forceinline__ uint32_t ancestor_bits(const int (&parr)[4], int node
 }
 
 // One 32-token tile staged in LDS (K rows at a pitch of D + 8 halves, V
-// rows at D + 16): S^T = K Q^T as two MFMA chains over the k-steps, the
+// rows at D + 16): S^T = K Q^T as one MFMA chain over the k-steps, the
 // masked online-softmax update of (m, l, acc), and O^T += V^T P^T with P as
 // an FP16 hi/lo pair.  kr is this lane's K row (token lr), vtr its
 // transpose-read address in the V rows, qB the Q^T B operand and okbits the
@@ -512,22 +512,19 @@ __device__ __forceinline__ void tile_math(const _Float16* kr, const _Float16* vt
   constexpr int KS = D / 16;
   constexpr int DT = D / 32;
   constexpr int VP = D + 16;
-  f32x16 sc0, sc1;
+  f32x16 sc;
 #pragma unroll
-  for (int j = 0; j < 16; ++j) sc0[j] = sc1[j] = 0.f;
+  for (int j = 0; j < 16; ++j) sc[j] = 0.f;
 #pragma unroll
-  for (int s = 0; s < KS; s += 2) {
+  for (int s = 0; s < KS; ++s) {
     const uint4 k0 = *reinterpret_cast<const uint4*>(kr + 16 * s + 8 * g);
-    const uint4 k1 = *reinterpret_cast<const uint4*>(kr + 16 * (s + 1) + 8 * g);
-    sc0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_f16x8(k0), as_f16x8(qB[s]), sc0, 0, 0, 0);
-    sc1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_f16x8(k1), as_f16x8(qB[s + 1]), sc1, 0, 0,
-                                                 0);
+    sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_f16x8(k0), as_f16x8(qB[s]), sc, 0, 0, 0);
   }
   // sc[j] holds token row 8*(j/4) + 4*g + j%4.  Scores stay unscaled here;
   // the scale enters the running max once and the exp2 argument as an FMA.
   float sv[16];
 #pragma unroll
-  for (int j = 0; j < 16; ++j) sv[j] = sc0[j] + sc1[j];
+  for (int j = 0; j < 16; ++j) sv[j] = sc[j];
   if (__builtin_amdgcn_ballot_w64(okbits != ~0u)) {  // masked tokens in the tile
     const uint32_t ob = okbits >> (4 * g);
 #pragma unroll
