@@ -720,19 +720,28 @@ __global__ __launch_bounds__(64 * W, 2) void tree_split_kernel(TreeParams P) {
     rowok = 0;
     if (it >= 0) {
       const int tb = it * kTile;
+      const bool okp0 = ph[0] >= 0 && ph[0] < P.phys_pages;
+      const bool okp1 = ph[1] >= 0 && ph[1] < P.phys_pages;
+      const bool whole = okp0 && okp1 && tb + kTile <= len;  // uniform: every row valid
 #pragma unroll
       for (int q = 0; q < 2; ++q) {
-        const bool okp = ph[q] >= 0 && ph[q] < P.phys_pages;
+        const bool okp = q ? okp1 : okp0;
         const size_t base = (size_t)(okp ? ph[q] : 0) * page_elems + (size_t)kvh * D;
         const char* kb = reinterpret_cast<const char*>(P.k + base);
         const char* vb = reinterpret_cast<const char*>(P.v + base);
 #pragma unroll
         for (int j = 0; j < LPP; ++j) {
           const int s = q * LPP + j;
-          rowok |= okp && tb + s * RPI + lrow < len ? 1u << s : 0u;
           kreg[s] = *reinterpret_cast<const uint4*>(kb + loff[j]);
           vreg[s] = *reinterpret_cast<const uint4*>(vb + loff[j]);
         }
+      }
+      if (whole) {
+        rowok = kAllRows;
+      } else {
+#pragma unroll
+        for (int s = 0; s < KS; ++s)
+          rowok |= (s < LPP ? okp0 : okp1) && tb + s * RPI + lrow < len ? 1u << s : 0u;
       }
     } else {
 #pragma unroll
