@@ -1135,16 +1135,21 @@ __global__ __launch_bounds__(kThreads, 2) void tree_rows_kernel(TreeParams P) {
       sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_f16x8(ka), as_f16x8(qB[s]), sc, 0, 0, 0);
     }
     // ---- mask and online softmax (column lr = query row) ----
-    const uint32_t ob = okbits >> (4 * g);
+    // Scores stay unscaled: the scale enters the running max once and the
+    // exp2 argument as an FMA; fully valid tiles skip the mask.
     float svv[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) svv[j] = sc[j];
+    if (__builtin_amdgcn_ballot_w64(okbits != ~0u)) {
+      const uint32_t ob = okbits >> (4 * g);
+#pragma unroll
+      for (int j = 0; j < 16; ++j)
+        svv[j] = (ob >> (8 * (j >> 2) + (j & 3))) & 1u ? svv[j] : kNegInf;
+    }
     float tmax = kNegInf;
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const bool ok = (ob >> (8 * (j >> 2) + (j & 3))) & 1u;
-      svv[j] = ok ? sc[j] * P.scale_log2 : kNegInf;
-      tmax = __builtin_fmaxf(tmax, svv[j]);
-    }
-    tmax = __builtin_fmaxf(tmax, shfl_xor_f(tmax, 32));
+    for (int j = 0; j < 16; ++j) tmax = __builtin_fmaxf(tmax, svv[j]);
+    tmax = __builtin_fmaxf(tmax, shfl_xor_f(tmax, 32)) * P.scale_log2;
     const float mnew = __builtin_fmaxf(m, tmax);
     if (__builtin_amdgcn_ballot_w64(mnew > m + kRescaleSlack)) {
       const float alpha = fast_exp2(m - safe_max(mnew));
@@ -1159,7 +1164,7 @@ __global__ __launch_bounds__(kThreads, 2) void tree_rows_kernel(TreeParams P) {
     f16x8 pb[2], pl[2];
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
-      const float pr = fast_exp2(svv[j] - mb);
+      const float pr = fast_exp2(__builtin_fmaf(svv[j], P.scale_log2, -mb));
       l += pr;
       const _Float16 hi = (_Float16)pr;
       pb[j >> 3][j & 7] = hi;
