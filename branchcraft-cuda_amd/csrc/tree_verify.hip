@@ -1371,16 +1371,16 @@ TreeParams make_params(const bc_shape& s, const bc_tree_inputs& in, int nodes) {
 // both measured slower at 8 x 2053 tokens (22.7 against 20.9 us): each
 // workgroup's fixed start, merge and partial-write cost outweighs the
 // second wave per SIMD.
-// tree_rows_kernel (one K/V tile shared by four row tiles) pays once
-// tree_kernel would run two or more workgroups per CU reading the prefix
-// once per row tile: at 8 requests of a 2048-token prefix, 64 nodes took 64
-// against 69 us and 256 nodes 164 against 273 us.  With fewer row tiles, or
-// without a workspace and fewer row groups than CUs, its serial walk over
-// the tiles lost (one request, 32 nodes, no workspace: 101 against 36 us).
-bool rows_kernel_for(int batch, int hkv, int row_tiles, bool workspace, int cus) {
-  if (row_tiles < kWaves) return false;
-  if ((long long)batch * hkv * row_tiles < 2LL * cus) return false;
-  return workspace ||
+// tree_rows_kernel (one K/V tile shared by four row tiles) pays once its
+// row groups fill the CUs: the split kernel would then run several rounds
+// of workgroups that each read the prefix for one row tile (8 requests x
+// 2048 tokens x 256 nodes: 153 against 206 us; 32 x 512 x 64 nodes: 48
+// against 78 us).  With fewer row groups the split kernel wins (8 x 2048 x
+// 64 nodes: 50 against 59 us; 4 x 2048 x 128: 52 against 58 us), and with
+// fewer than four row tiles the rows kernel's serial walk lost outright
+// (one request, 32 nodes: 101 against 36 us).
+bool rows_kernel_for(int batch, int hkv, int row_tiles, int cus) {
+  return row_tiles >= kWaves &&
          (long long)batch * hkv * ((row_tiles + kWaves - 1) / kWaves) >= cus;
 }
 
@@ -1433,8 +1433,7 @@ void launch_tree_kernel(const TreeParams& P, bool rows_kernel, dim3 grid, hipStr
 // vec: every FP16 tensor and the output are 16-byte aligned (16-byte loads
 // and stores); otherwise the kernels move single halves and floats.
 hipError_t launch_tree(TreeParams& P, int dim, int parts, bool vec, hipStream_t st) {
-  const bool rows_kernel = rows_kernel_for(P.batch, P.hkv, P.row_tiles, P.part_acc != nullptr,
-                                           bch::device_cus());
+  const bool rows_kernel = rows_kernel_for(P.batch, P.hkv, P.row_tiles, bch::device_cus());
   const dim3 grid(
       (unsigned)((size_t)parts * P.batch * P.hkv * row_units(P.row_tiles, rows_kernel)));
   if (dim == 64) {
@@ -1578,7 +1577,7 @@ extern "C" int bc_tree_verify(bc_shape s, bc_tree_inputs in, int nodes,
   const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const bool vec = tree_ptrs_aligned(in);
   const int cus = bch::device_cus();
-  if (vec && !rows_kernel_for(P.batch, P.hkv, P.row_tiles, false, cus)) {
+  if (vec && !rows_kernel_for(P.batch, P.hkv, P.row_tiles, cus)) {
     const int max_tiles =
         (s.max_pages * BC_PAGE_SIZE + kTile - 1) / kTile + (nodes + kTile - 1) / kTile;
     const long long units = (long long)P.batch * P.hkv * P.row_tiles;
@@ -1599,7 +1598,7 @@ bool tree_shape_ok(const bc_shape& s, int nodes) {
 
 bool split_for(const bc_shape& s, int nodes) {
   const int row_tiles = (nodes * (s.query_heads / s.kv_heads) + 31) / 32;
-  return !rows_kernel_for(s.batch, s.kv_heads, row_tiles, true, bch::device_cus());
+  return !rows_kernel_for(s.batch, s.kv_heads, row_tiles, bch::device_cus());
 }
 
 size_t ws_size(const bc_shape& s, int nodes) {

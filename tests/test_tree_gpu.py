@@ -118,11 +118,12 @@ def test_mid_batch_splits_the_prefix(oracle):
     _check(fix, oracle, atol=3e-4, what="B=16")
 
 
-@pytest.mark.parametrize("batch,nodes,hq,hkv,d", [(8, 128, 32, 8, 128), (4, 64, 64, 8, 64)])
+@pytest.mark.parametrize("batch,nodes,hq,hkv,d", [(8, 128, 32, 8, 128), (8, 64, 64, 8, 64)])
 def test_large_trees_share_tiles_across_row_tiles(batch, nodes, hq, hkv, d, oracle):
-    """Trees of 16 row tiles per (request, KV head) with at least two
-    row-tile units per CU take tree_rows_kernel, which loads each K/V tile
-    once for four row tiles (with and without a workspace)."""
+    """Trees of 16 row tiles per (request, KV head) whose groups of four row
+    tiles fill the CUs (8 requests x 8 KV heads x 4 groups) take
+    tree_rows_kernel, which loads each K/V tile once for four row tiles
+    (the workspace entry point runs it too: it needs no workspace)."""
     rng = np.random.default_rng(nodes + d)
     fix = oracle_np.tree_fixture(rng, batch, 300, nodes, hq=hq, hkv=hkv, d=d,
                                  parents="random")
