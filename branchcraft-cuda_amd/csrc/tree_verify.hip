@@ -29,8 +29,7 @@
 //    pages run on the same XCD and reuse its L2.
 //  - tree_rows_kernel: trees of many row tiles per (request, KV head), whose
 //    units already fill the CUs: four waves take four row tiles and walk the
-//    same K/V tiles, loaded once per workgroup; merge_tree_kernel combines
-//    its prefix chunks.
+//    same K/V tiles, loaded once per workgroup.
 //  - tree_kernel: the single pass for tensors that are not 16-byte aligned
 //    (element-wise loads and stores).
 #include "bc_device.h"
@@ -62,12 +61,10 @@ struct TreeParams {
   const uint16_t* dv;       // draft V
   const int32_t* parent;    // [B,N]
   float* out;               // [B,N,Hq,D]
-  float* part_acc;          // workspace partials (null: one unit per row tile)
+  float* part_acc;          // split-kernel partials (null: one part per unit)
   float* part_ml;
   int batch, nodes, hq, hkv, group, max_pages, phys_pages;
   int rows, row_tiles;      // rows = nodes * group per (request, KV head)
-  int chunk_tokens;         // prefix tokens per chunk (workspace mode)
-  int prefix_parts;         // chunk slots per row; slot prefix_parts = drafts
   float scale_log2;
   // tree_split_kernel: parts per unit and tiles per part; with parts > 1,
   // part_acc/part_ml hold P.parts slots per output row.
@@ -86,11 +83,6 @@ __device__ __forceinline__ f16x4 lds_read_tr(const _Float16* p) {
   return __builtin_bit_cast(f16x4, r);
 }
 
-__device__ __forceinline__ size_t slot_index(const TreeParams& P, int b,
-                                             int node, int h, int part) {
-  return (((size_t)b * P.nodes + node) * P.hq + h) * (P.prefix_parts + 1) + part;
-}
-
 template <int D, bool VEC>
 __global__ __launch_bounds__(kThreads, 2) void tree_kernel(TreeParams P) {
   constexpr int KS = D / 16;  // MFMA k-steps over the head dimension
@@ -104,8 +96,7 @@ __global__ __launch_bounds__(kThreads, 2) void tree_kernel(TreeParams P) {
 
   const int zdim = P.hkv * P.row_tiles;
   const int z = blockIdx.x % zdim;
-  const int b = (blockIdx.x / zdim) % P.batch;
-  const int part = blockIdx.x / (zdim * P.batch);
+  const int b = blockIdx.x / zdim;
   const int kvh = z / P.row_tiles;
   const int rt = z % P.row_tiles;
 
@@ -113,32 +104,14 @@ __global__ __launch_bounds__(kThreads, 2) void tree_kernel(TreeParams P) {
   // length (they do not depend on it) so the first K/V loads wait for one
   // memory round trip instead of two.
   int ida[2];
-  {
-    const int tp0s = P.part_acc && part < P.prefix_parts ? part * P.chunk_tokens / kTile : 0;
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
-      const int pg = (tp0s + wave) * (kTile / BC_PAGE_SIZE) + q;
-      ida[q] = pg < P.max_pages ? P.pages[(size_t)b * P.max_pages + pg] : -1;
-    }
+  for (int q = 0; q < 2; ++q) {
+    const int pg = wave * (kTile / BC_PAGE_SIZE) + q;
+    ida[q] = pg < P.max_pages ? P.pages[(size_t)b * P.max_pages + pg] : -1;
   }
   const int len = max(0, min(P.lengths[b], P.max_pages * BC_PAGE_SIZE));
-  int pbeg = 0, pend = len;
-  bool drafts = true, final_out = true;
-  if (P.part_acc) {
-    const int nparts = (len + P.chunk_tokens - 1) / P.chunk_tokens;
-    if (part < P.prefix_parts) {
-      if (part >= nparts) return;  // uniform over the workgroup
-      pbeg = part * P.chunk_tokens;
-      pend = min(pbeg + P.chunk_tokens, len);
-      drafts = false;
-    } else {
-      pend = 0;
-    }
-    final_out = nparts == 0;
-  }
-  const int tp0 = pbeg / kTile;
-  const int ntile_p = pend > pbeg ? (pend - 1) / kTile - tp0 + 1 : 0;
-  const int ntile_d = drafts ? (P.nodes + kTile - 1) / kTile : 0;
+  const int ntile_p = (len + kTile - 1) / kTile;
+  const int ntile_d = (P.nodes + kTile - 1) / kTile;
 
   // This lane's query row (tile column lr).
   const int r = rt * 32 + lr;
@@ -195,7 +168,7 @@ __global__ __launch_bounds__(kThreads, 2) void tree_kernel(TreeParams P) {
     const int it = tile_of(idx);
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
-      const int pg = (tp0 + it) * (kTile / BC_PAGE_SIZE) + q;
+      const int pg = it * (kTile / BC_PAGE_SIZE) + q;
       ph[q] = it < ntile_p && pg < P.max_pages ? P.pages[(size_t)b * P.max_pages + pg] : -1;
     }
   };
@@ -206,11 +179,11 @@ __global__ __launch_bounds__(kThreads, 2) void tree_kernel(TreeParams P) {
     const int it = tile_of(idx);
     const uint16_t* kp;
     if (it < ntile_p) {
-      const int tbase = (tp0 + it) * kTile;
+      const int tbase = it * kTile;
 #pragma unroll
       for (int q = 0; q < 2; ++q) pok[q] = ph[q] >= 0 && ph[q] < P.phys_pages;
       const int t = tbase + lr;
-      tv = t >= pbeg && t < pend && pok[lr >> 4];
+      tv = t < len && pok[lr >> 4];
       const size_t phys = (size_t)(tv ? (lr >> 4 ? ph[1] : ph[0]) : 0);
       const size_t off =
           tv ? (phys * BC_PAGE_SIZE + t % BC_PAGE_SIZE) * tok_stride + (size_t)kvh * D : 0;
@@ -236,17 +209,16 @@ __global__ __launch_bounds__(kThreads, 2) void tree_kernel(TreeParams P) {
     for (int s = 0; s < KS; ++s) vr[s] = load8<VEC>(vp + 16 * s + 8 * g);
     const int it = wave + kWaves * idx;
     const bool is_draft = it >= ntile_p;
-    const int tbase = is_draft ? (it - ntile_p) * kTile : (tp0 + it) * kTile;
+    const int tbase = (is_draft ? it - ntile_p : it) * kTile;
     // Valid token rows of the tile as a bit mask (bit i = token tbase + i):
-    // prefix tiles clip [pbeg, pend) and drop pages outside the pool (uniform
-    // over the wave); draft tiles take this row's ancestor-or-self set.
+    // prefix tiles stop at the length and drop pages outside the pool
+    // (uniform over the wave); draft tiles take this row's ancestor-or-self
+    // set.
     uint32_t okbits;
     if (!is_draft) {
-      const int lo = min(max(pbeg - tbase, 0), kTile);
-      const int hi = min(max(pend - tbase, 0), kTile);
-      const uint32_t below_hi = hi >= kTile ? ~0u : (1u << hi) - 1u;
-      const uint32_t below_lo = lo >= kTile ? ~0u : (1u << lo) - 1u;
-      okbits = (below_hi & ~below_lo) & ((pok[0] ? 0x0000ffffu : 0u) | (pok[1] ? 0xffff0000u : 0u));
+      const int hi = min(max(len - tbase, 0), kTile);
+      okbits = (hi >= kTile ? ~0u : (1u << hi) - 1u) &
+               ((pok[0] ? 0x0000ffffu : 0u) | (pok[1] ? 0xffff0000u : 0u));
     } else {
       okbits = 0;
       int cur = node;
@@ -431,32 +403,15 @@ __global__ __launch_bounds__(kThreads, 2) void tree_kernel(TreeParams P) {
   if (!rvalid) return;
 
   // ---- write: lane holds O^T[32dt + 8jq + 4g + e][row r] ----
-  if (final_out) {
-    float* dst = P.out + (((size_t)b * P.nodes + node) * P.hq + h) * D;
-    const float inv = 1.f / l;
+  float* dst = P.out + (((size_t)b * P.nodes + node) * P.hq + h) * D;
+  const float inv = 1.f / l;
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
+  for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-      for (int jq = 0; jq < 4; ++jq)
-        store4f<VEC>(dst + 32 * dt + 8 * jq + 4 * g, acc[dt][4 * jq] * inv,
-                     acc[dt][4 * jq + 1] * inv, acc[dt][4 * jq + 2] * inv,
-                     acc[dt][4 * jq + 3] * inv);
-  } else {
-    const int p = drafts ? P.prefix_parts : part;
-    const size_t slot = slot_index(P, b, node, h, p);
-    float* dst = P.part_acc + slot * D;
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-      for (int jq = 0; jq < 4; ++jq)
-        *reinterpret_cast<float4*>(dst + 32 * dt + 8 * jq + 4 * g) =
-            make_float4(acc[dt][4 * jq], acc[dt][4 * jq + 1], acc[dt][4 * jq + 2],
-                        acc[dt][4 * jq + 3]);
-    if (g == 0) {
-      P.part_ml[2 * slot] = m;
-      P.part_ml[2 * slot + 1] = l;
-    }
-  }
+    for (int jq = 0; jq < 4; ++jq)
+      store4f<VEC>(dst + 32 * dt + 8 * jq + 4 * g, acc[dt][4 * jq] * inv,
+                   acc[dt][4 * jq + 1] * inv, acc[dt][4 * jq + 2] * inv,
+                   acc[dt][4 * jq + 3] * inv);
 }
 
 // ---- per-tile pieces of tree_split_kernel ----
@@ -987,29 +942,13 @@ __global__ __launch_bounds__(kThreads, 2) void tree_rows_kernel(TreeParams P) {
   const int rgroups = (P.row_tiles + kWaves - 1) / kWaves;
   const int zdim = P.hkv * rgroups;
   const int z = blockIdx.x % zdim;
-  const int b = (blockIdx.x / zdim) % P.batch;
-  const int part = blockIdx.x / (zdim * P.batch);
+  const int b = blockIdx.x / zdim;
   const int kvh = z / rgroups;
   const int rt = (z % rgroups) * kWaves + wave;  // row tile; idle when >= row_tiles
 
   const int len = max(0, min(P.lengths[b], P.max_pages * BC_PAGE_SIZE));
-  int pbeg = 0, pend = len;
-  bool drafts = true, final_out = true;
-  if (P.part_acc) {
-    const int nparts = (len + P.chunk_tokens - 1) / P.chunk_tokens;
-    if (part < P.prefix_parts) {
-      if (part >= nparts) return;  // uniform over the workgroup
-      pbeg = part * P.chunk_tokens;
-      pend = min(pbeg + P.chunk_tokens, len);
-      drafts = false;
-    } else {
-      pend = 0;
-    }
-    final_out = nparts == 0;
-  }
-  const int tp0 = pbeg / kTile;
-  const int ntile_p = pend > pbeg ? (pend - 1) / kTile - tp0 + 1 : 0;
-  const int ntile = ntile_p + (drafts ? (P.nodes + kTile - 1) / kTile : 0);
+  const int ntile_p = (len + kTile - 1) / kTile;
+  const int ntile = ntile_p + (P.nodes + kTile - 1) / kTile;
 
   const int r = rt * 32 + lr;
   const bool rvalid = rt < P.row_tiles && r < P.rows;
@@ -1042,14 +981,14 @@ __global__ __launch_bounds__(kThreads, 2) void tree_rows_kernel(TreeParams P) {
   auto page_ids = [&](int i, int (&pg)[2]) {
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
-      const int pi = (tp0 + i) * (kTile / BC_PAGE_SIZE) + q;
+      const int pi = i * (kTile / BC_PAGE_SIZE) + q;
       pg[q] = i < ntile_p && pi < P.max_pages ? P.pages[(size_t)b * P.max_pages + pi] : -1;
     }
   };
   auto load_tile = [&](int i, int set) {
     const int (&pg)[2] = ph[set];
     const bool is_draft = i >= ntile_p;
-    const int tbase = is_draft ? (i - ntile_p) * kTile : (tp0 + i) * kTile;
+    const int tbase = (is_draft ? i - ntile_p : i) * kTile;
 #pragma unroll
     for (int c = 0; c < CPT; ++c) {
       const int chunk = (int)threadIdx.x + kThreads * c;
@@ -1060,7 +999,7 @@ __global__ __launch_bounds__(kThreads, 2) void tree_rows_kernel(TreeParams P) {
         const int pgq = pg[row / BC_PAGE_SIZE];
         const bool pok = pgq >= 0 && pgq < P.phys_pages;
         const int t = tbase + row;
-        ok = pok && t >= pbeg && t < pend;
+        ok = pok && t < len;
         off = (pok ? ((size_t)pgq * BC_PAGE_SIZE + row % BC_PAGE_SIZE) * tok_stride : 0) +
               (size_t)kvh * D + col;
         kreg[set][c] = load8<VEC>(P.k + off);
@@ -1108,14 +1047,11 @@ __global__ __launch_bounds__(kThreads, 2) void tree_rows_kernel(TreeParams P) {
     const _Float16* sk = s_kv + buf * BUF;
     const _Float16* sv = sk + kTile * KP;
     const bool is_draft = i >= ntile_p;
-    const int tbase = is_draft ? (i - ntile_p) * kTile : (tp0 + i) * kTile;
+    const int tbase = (is_draft ? i - ntile_p : i) * kTile;
     uint32_t okbits;
     if (!is_draft) {
-      const int lo = min(max(pbeg - tbase, 0), kTile);
-      const int hi = min(max(pend - tbase, 0), kTile);
-      const uint32_t below_hi = hi >= kTile ? ~0u : (1u << hi) - 1u;
-      const uint32_t below_lo = lo >= kTile ? ~0u : (1u << lo) - 1u;
-      okbits = (below_hi & ~below_lo) &
+      const int hi = min(max(len - tbase, 0), kTile);
+      okbits = (hi >= kTile ? ~0u : (1u << hi) - 1u) &
                ((s_pok[buf][0] ? 0x0000ffffu : 0u) | (s_pok[buf][1] ? 0xffff0000u : 0u));
     } else {
       okbits = 0;
@@ -1227,104 +1163,15 @@ __global__ __launch_bounds__(kThreads, 2) void tree_rows_kernel(TreeParams P) {
   l += shfl_xor_f(l, 32);
 
   // ---- write: lane holds O^T[32dt + 8jq + 4g + e][row r] ----
-  if (final_out) {
-    float* dst = P.out + (((size_t)b * P.nodes + node) * P.hq + h) * D;
-    const float inv = 1.f / l;
+  float* dst = P.out + (((size_t)b * P.nodes + node) * P.hq + h) * D;
+  const float inv = 1.f / l;
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
+  for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-      for (int jq = 0; jq < 4; ++jq)
-        store4f<VEC>(dst + 32 * dt + 8 * jq + 4 * g, acc[dt][4 * jq] * inv,
-                     acc[dt][4 * jq + 1] * inv, acc[dt][4 * jq + 2] * inv,
-                     acc[dt][4 * jq + 3] * inv);
-  } else {
-    const int p = drafts ? P.prefix_parts : part;
-    const size_t slot = slot_index(P, b, node, h, p);
-    float* dst = P.part_acc + slot * D;
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-      for (int jq = 0; jq < 4; ++jq)
-        *reinterpret_cast<float4*>(dst + 32 * dt + 8 * jq + 4 * g) =
-            make_float4(acc[dt][4 * jq], acc[dt][4 * jq + 1], acc[dt][4 * jq + 2],
-                        acc[dt][4 * jq + 3]);
-    if (g == 0) {
-      P.part_ml[2 * slot] = m;
-      P.part_ml[2 * slot + 1] = l;
-    }
-  }
-}
-
-// Combines the prefix chunks and the draft part of every (b, node, h): one
-// wave per output row, lane p reads slot p's (max, sum), the weights are
-// formed once and every lane accumulates its dims with independent loads.
-// Slot p < prefix_parts holds prefix chunk p, slot prefix_parts the draft
-// part.  The request's length only says how many prefix slots were written
-// (nparts), so the (max, sum) of every slot, the draft slot's accumulator
-// and the first eight prefix slots' go out together with the length, and
-// unwritten slots are masked afterwards by selects (their contents are
-// whatever the workspace held, NaN included).
-template <int D>
-__global__ __launch_bounds__(256) void merge_tree_kernel(TreeParams P) {
-  constexpr int PER = D / 64;
-  const int lane = threadIdx.x & 63;
-  const size_t row = (size_t)blockIdx.x * 4 + (threadIdx.x >> 6);  // (b*N+node)*Hq+h
-  if (row >= (size_t)P.batch * P.nodes * P.hq) return;
-  const int b = row / ((size_t)P.nodes * P.hq);
-  const int lraw = P.lengths[b];
-  const int dslot = P.prefix_parts;  // 2 <= prefix_parts <= 63 (tree_chunking)
-  const size_t base = row * (P.prefix_parts + 1);
-  auto load_slot = [&](int sidx, float (&v)[PER]) {
-    const float* src = P.part_acc + (base + sidx) * D + lane;
-#pragma unroll
-    for (int j = 0; j < PER; ++j) v[j] = src[64 * j];
-  };
-  const size_t ms = base + min(lane, dslot);
-  const float mp0 = P.part_ml[2 * ms], lp0 = P.part_ml[2 * ms + 1];
-  float vd[PER], v[8][PER];
-  load_slot(dslot, vd);
-#pragma unroll
-  for (int u = 0; u < 8; ++u) load_slot(min(u, dslot - 1), v[u]);
-#pragma unroll
-  for (int j = 0; j < PER; ++j) {
-    asm volatile("" ::"v"(vd[j]));
-#pragma unroll
-    for (int u = 0; u < 8; ++u) asm volatile("" ::"v"(v[u][j]));
-  }
-  const int len = max(0, min(lraw, P.max_pages * BC_PAGE_SIZE));
-  const int nparts = (len + P.chunk_tokens - 1) / P.chunk_tokens;
-  if (nparts == 0) return;  // the draft part wrote the final output
-  const bool written = lane < nparts || lane == dslot;
-  const float mp = written ? mp0 : kNegInf;
-  const float lp = written ? lp0 : 0.f;
-  const float mm = wave_max(mp);
-  const float w = fast_exp2(mp - mm);  // every row sees its own node: mm finite
-  const float lsum = wave_sum(w * lp);
-  auto weight = [&](int sidx) {
-    return __builtin_bit_cast(float,
-                              __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), sidx));
-  };
-  float a[PER];
-  const float wd = weight(dslot);
-#pragma unroll
-  for (int j = 0; j < PER; ++j) a[j] = wd * vd[j];
-  for (int i0 = 0; i0 < nparts; i0 += 8) {
-    if (i0 > 0) {
-#pragma unroll
-      for (int u = 0; u < 8; ++u) load_slot(min(i0 + u, nparts - 1), v[u]);
-    }
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      if (i0 + u < nparts) {  // uniform
-        const float wi = weight(i0 + u);
-#pragma unroll
-        for (int j = 0; j < PER; ++j) a[j] += wi * v[u][j];
-      }
-    }
-  }
-  const float inv = 1.f / lsum;
-#pragma unroll
-  for (int j = 0; j < PER; ++j) P.out[row * D + lane + 64 * j] = a[j] * inv;
+    for (int jq = 0; jq < 4; ++jq)
+      store4f<VEC>(dst + 32 * dt + 8 * jq + 4 * g, acc[dt][4 * jq] * inv,
+                   acc[dt][4 * jq + 1] * inv, acc[dt][4 * jq + 2] * inv,
+                   acc[dt][4 * jq + 3] * inv);
 }
 
 bool tree_args_ok(const bc_shape& s, const bc_tree_inputs& in, int nodes) {
@@ -1365,12 +1212,6 @@ TreeParams make_params(const bc_shape& s, const bc_tree_inputs& in, int nodes) {
   return P;
 }
 
-// Prefix chunking for the workspace path: about one workgroup per CU,
-// counting the draft part of every unit, chunks of at least 128 tokens,
-// multiples of 32.  Two workgroups fit a CU, but halving the chunks to fill
-// both measured slower at 8 x 2053 tokens (22.7 against 20.9 us): each
-// workgroup's fixed start, merge and partial-write cost outweighs the
-// second wave per SIMD.
 // tree_rows_kernel (one K/V tile shared by four row tiles) pays once its
 // row groups fill the CUs: the split kernel would then run several rounds
 // of workgroups that each read the prefix for one row tile (8 requests x
@@ -1384,42 +1225,9 @@ bool rows_kernel_for(int batch, int hkv, int row_tiles, int cus) {
          (long long)batch * hkv * ((row_tiles + kWaves - 1) / kWaves) >= cus;
 }
 
-// Workgroups per (request, KV head, prefix chunk).
+// Workgroups per (request, KV head).
 int row_units(int row_tiles, bool rows_kernel) {
   return rows_kernel ? (row_tiles + kWaves - 1) / kWaves : row_tiles;
-}
-
-// Prefix tokens per chunk for `want` chunks: multiples of 32, at least
-// `floor`, and at most 63 chunks (the merge reads one partial per lane).
-int chunk_for(int max_tokens, long long want, int floor = 128) {
-  if (want < 1) want = 1;
-  int chunk = (int)((max_tokens + want - 1) / want);
-  chunk = (chunk + kTile - 1) / kTile * kTile;
-  if (chunk < floor) chunk = floor;
-  const int min_chunk = (max_tokens + 62) / 63;
-  if (chunk < min_chunk) chunk = (min_chunk + kTile - 1) / kTile * kTile;
-  return chunk;
-}
-
-// Prefix chunks of the workspace path of tree_rows_kernel (large trees): it
-// walks its tiles in series, so it takes two workgroups per CU (two fit).
-void tree_chunking(const bc_shape& s, int nodes, int* chunk_tokens, int* parts) {
-  const int group = s.query_heads / s.kv_heads;
-  const int row_tiles = (nodes * group + 31) / 32;
-  const int cus = bch::device_cus();
-  const int max_tokens = s.max_pages * BC_PAGE_SIZE;
-  const long long units = (long long)s.batch * s.kv_heads * row_units(row_tiles, true);
-  const int chunk = chunk_for(max_tokens, 2LL * cus / units - 1);
-  *chunk_tokens = chunk;
-  *parts = (max_tokens + chunk - 1) / chunk;
-}
-
-size_t tree_workspace(const bc_shape& s, int nodes, int* chunk_tokens, int* parts) {
-  tree_chunking(s, nodes, chunk_tokens, parts);
-  if (*parts <= 1) return 0;
-  const size_t slots = (size_t)s.batch * nodes * s.query_heads * (*parts + 1);
-  const size_t acc = (slots * s.dim * sizeof(float) + 255) & ~(size_t)255;
-  return acc + slots * 2 * sizeof(float);
 }
 
 template <int D, bool VEC>
@@ -1432,10 +1240,9 @@ void launch_tree_kernel(const TreeParams& P, bool rows_kernel, dim3 grid, hipStr
 
 // vec: every FP16 tensor and the output are 16-byte aligned (16-byte loads
 // and stores); otherwise the kernels move single halves and floats.
-hipError_t launch_tree(TreeParams& P, int dim, int parts, bool vec, hipStream_t st) {
+hipError_t launch_tree(const TreeParams& P, int dim, bool vec, hipStream_t st) {
   const bool rows_kernel = rows_kernel_for(P.batch, P.hkv, P.row_tiles, bch::device_cus());
-  const dim3 grid(
-      (unsigned)((size_t)parts * P.batch * P.hkv * row_units(P.row_tiles, rows_kernel)));
+  const dim3 grid((unsigned)((size_t)P.batch * P.hkv * row_units(P.row_tiles, rows_kernel)));
   if (dim == 64) {
     if (vec) launch_tree_kernel<64, true>(P, rows_kernel, grid, st);
     else launch_tree_kernel<64, false>(P, rows_kernel, grid, st);
@@ -1443,12 +1250,6 @@ hipError_t launch_tree(TreeParams& P, int dim, int parts, bool vec, hipStream_t 
     if (vec) launch_tree_kernel<128, true>(P, rows_kernel, grid, st);
     else launch_tree_kernel<128, false>(P, rows_kernel, grid, st);
   }
-  hipError_t err = hipGetLastError();
-  if (err != hipSuccess || !P.part_acc) return err;
-  const size_t rows = (size_t)P.batch * P.nodes * P.hq;
-  const dim3 mgrid((unsigned)((rows + 3) / 4));
-  if (dim == 64) merge_tree_kernel<64><<<mgrid, 256, 0, st>>>(P);
-  else merge_tree_kernel<128><<<mgrid, 256, 0, st>>>(P);
   return hipGetLastError();
 }
 
@@ -1573,7 +1374,6 @@ extern "C" int bc_tree_verify(bc_shape s, bc_tree_inputs in, int nodes,
                               bc_stream_t stream) {
   if (!tree_args_ok(s, in, nodes)) return BC_ERROR_INVALID_VALUE;
   TreeParams P = make_params(s, in, nodes);
-  P.prefix_parts = 0;
   const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const bool vec = tree_ptrs_aligned(in);
   const int cus = bch::device_cus();
@@ -1584,7 +1384,7 @@ extern "C" int bc_tree_verify(bc_shape s, bc_tree_inputs in, int nodes,
     return launch_split(P, s.dim, pair_requests(P.batch, units, SplitPlan{1, max_tiles, 8}, cus),
                         nullptr, 0, st);
   }
-  return launch_tree(P, s.dim, 1, vec, st);
+  return launch_tree(P, s.dim, vec, st);
 }
 
 namespace {
@@ -1601,13 +1401,11 @@ bool split_for(const bc_shape& s, int nodes) {
   return !rows_kernel_for(s.batch, s.kv_heads, row_tiles, bch::device_cus());
 }
 
+// tree_rows_kernel and split plans of one part need no workspace.
 size_t ws_size(const bc_shape& s, int nodes) {
-  if (split_for(s, nodes)) {
-    size_t a = 0;
-    return split_workspace(s, nodes, split_plan(s, nodes, bch::device_cus()), &a);
-  }
-  int chunk = 0, parts = 0;
-  return tree_workspace(s, nodes, &chunk, &parts);
+  if (!split_for(s, nodes)) return 0;
+  size_t a = 0;
+  return split_workspace(s, nodes, split_plan(s, nodes, bch::device_cus()), &a);
 }
 
 int tree_ws_call(bc_shape s, bc_tree_inputs in, int nodes, void* workspace,
@@ -1616,28 +1414,14 @@ int tree_ws_call(bc_shape s, bc_tree_inputs in, int nodes, void* workspace,
   const bool vec = tree_ptrs_aligned(in);
   // Tensors that are not 16-byte aligned take the element-wise single pass.
   if (!vec) return bc_tree_verify(s, in, nodes, stream);
-  const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  if (split_for(s, nodes)) {
-    const SplitPlan plan = split_plan(s, nodes, bch::device_cus());
-    size_t acc = 0;
-    const size_t need = split_workspace(s, nodes, plan, &acc);
-    if (!workspace || need == 0 || workspace_bytes < need || !aligned16(workspace))
-      return bc_tree_verify(s, in, nodes, stream);
-    TreeParams P = make_params(s, in, nodes);
-    return launch_split(P, s.dim, plan, workspace, acc, st);
-  }
-  int chunk = 0, parts = 0;
-  const size_t need = tree_workspace(s, nodes, &chunk, &parts);
+  if (!split_for(s, nodes)) return bc_tree_verify(s, in, nodes, stream);
+  const SplitPlan plan = split_plan(s, nodes, bch::device_cus());
+  size_t acc = 0;
+  const size_t need = split_workspace(s, nodes, plan, &acc);
   if (!workspace || need == 0 || workspace_bytes < need || !aligned16(workspace))
     return bc_tree_verify(s, in, nodes, stream);
   TreeParams P = make_params(s, in, nodes);
-  P.chunk_tokens = chunk;
-  P.prefix_parts = parts;
-  const size_t slots = (size_t)s.batch * nodes * s.query_heads * (parts + 1);
-  const size_t acc = (slots * s.dim * sizeof(float) + 255) & ~(size_t)255;
-  P.part_acc = static_cast<float*>(workspace);
-  P.part_ml = reinterpret_cast<float*>(static_cast<char*>(workspace) + acc);
-  return launch_tree(P, s.dim, parts + 1, true, st);
+  return launch_split(P, s.dim, plan, workspace, acc, reinterpret_cast<hipStream_t>(stream));
 }
 
 }  // namespace

@@ -124,9 +124,9 @@ int bc_tree_verify(bc_shape shape, bc_tree_inputs in, int nodes,
  * shape does not benefit from splitting the prefix). */
 size_t bc_tree_verify_workspace_size(bc_shape shape, int nodes);
 
-/* bc_tree_verify with the prefix split into chunks across workgroups and an
- * FP32 merge; `workspace` holds at least bc_tree_verify_workspace_size
- * bytes.  A null workspace, one smaller than required or one not aligned to
+/* bc_tree_verify with each request's tiles split over several workgroups
+ * and an FP32 merge; `workspace` holds at least
+ * bc_tree_verify_workspace_size bytes.  A null workspace, one smaller than required or one not aligned to
  * 16 bytes falls back to bc_tree_verify.  Results match bc_tree_verify
  * within floating-point reassociation. */
 int bc_tree_verify_ws(bc_shape shape, bc_tree_inputs in, int nodes,

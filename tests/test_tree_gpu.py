@@ -107,8 +107,8 @@ def test_garbage_past_prefix_is_ignored(oracle):
 
 def test_mid_batch_splits_the_prefix(oracle):
     """Sixteen requests: 128 (request, KV head, row tile) units, half the
-    CUs, so the workspace call splits each prefix in two chunks plus the
-    draft part."""
+    CUs, so the workspace call splits each unit's tiles over several
+    workgroups and merges their partials."""
     rng = np.random.default_rng(16)
     fix = oracle_np.tree_fixture(rng, 16, 700, 7, parents="random")
     k, v, pages, lengths, dq, dk, dv, par = fix
