@@ -166,16 +166,18 @@ def _group_fixture(rng, lengths, share, nodes=7, hq=32, hkv=8, d=128, cow_last=(
     # request 0's, 10 has its own (a last group of three)
     dict(lengths=[613, 613, 613, 400, 613, 613, 613, 613, 613, 613, 250],
          share=[-1, 0, 0, 0, -1, 4, 4, 4, 0, 0, -1], cow_last=(5,)),
-    # nine requests on one page table (a last group of one)
-    dict(lengths=[300] * 9, share=[-1] + [0] * 8),
+    # nine requests on one page table (a last group of one); the spare
+    # page-table capacity of this and other short cases keeps them above
+    # sixteen tiles, where the workspace call splits
+    dict(lengths=[300] * 9, share=[-1] + [0] * 8, extra_pages=12),
     # empty requests beside sharing ones (their drafts give the output)
-    dict(lengths=[300, 0, 300, 300, 300, 300, 0, 300], share=[-1] + [0] * 7),
+    dict(lengths=[300, 0, 300, 300, 300, 300, 0, 300], share=[-1] + [0] * 7, extra_pages=12),
     # page tables far longer than every request (empty prefix chunks)
     dict(lengths=[100] * 8, share=[-1] + [0] * 7, extra_pages=38),
     # D = 64, group 4, eight nodes (32 rows)
     dict(lengths=[517] * 8, share=[-1] + [0] * 7, nodes=8, hq=8, hkv=2, d=64),
     # group 1: 32 nodes fill the row tile and the draft tile
-    dict(lengths=[290] * 8, share=[-1] + [0] * 7, nodes=32, hq=8, hkv=8),
+    dict(lengths=[290] * 8, share=[-1] + [0] * 7, nodes=32, hq=8, hkv=8, extra_pages=12),
     # five requests, two page tables
     dict(lengths=[613, 613, 400, 613, 613], share=[-1, 0, 0, -1, 3]),
 ])
