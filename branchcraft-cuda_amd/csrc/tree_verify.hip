@@ -32,6 +32,8 @@
 //    same K/V tiles, loaded once per workgroup.
 //  - tree_kernel: the single pass for tensors that are not 16-byte aligned
 //    (element-wise loads and stores).
+#include <type_traits>
+
 #include "bc_device.h"
 #include "bc_host.h"
 
@@ -454,19 +456,19 @@ __device__ __forceinline__ uint32_t ancestor_bits(const int (&parr)[4], int node
 }
 
 // One 32-token tile staged in LDS (K rows at a pitch of D + 8 halves, V
-// rows at D + 16): S^T = K Q^T as one MFMA chain over the k-steps, the
-// masked online-softmax update of (m, l, acc), and O^T += V^T P^T with P as
-// an FP16 hi/lo pair.  kr is this lane's K row (token lr), vtr its
-// transpose-read address in the V rows, qB the Q^T B operand and okbits the
-// valid tokens of the lane's query row.
+// rows at D + 16), in two steps.  tile_scores: S^T = K Q^T as one MFMA
+// chain over the k-steps and the masked online-softmax update of (m, l,
+// acc), leaving P as an FP16 hi/lo pair; tile_pv: O^T += V^T P^T.  kr is
+// this lane's K row (token lr), vtr its transpose-read address in the V
+// rows, qB the Q^T B operand and okbits the valid tokens of the lane's
+// query row.
 template <int D>
-__device__ __forceinline__ void tile_math(const _Float16* kr, const _Float16* vtr,
-                                          const uint4 (&qB)[D / 16], uint32_t okbits,
-                                          float scale_log2, int g, f32x16 (&acc)[D / 32],
-                                          float& m, float& l) {
+__device__ __forceinline__ void tile_scores(const _Float16* kr, const uint4 (&qB)[D / 16],
+                                            uint32_t okbits, float scale_log2, int g,
+                                            f32x16 (&acc)[D / 32], float& m, float& l,
+                                            f16x8 (&pb)[2], f16x8 (&pl)[2]) {
   constexpr int KS = D / 16;
   constexpr int DT = D / 32;
-  constexpr int VP = D + 16;
   f32x16 sc;
 #pragma unroll
   for (int j = 0; j < 16; ++j) sc[j] = 0.f;
@@ -504,7 +506,6 @@ __device__ __forceinline__ void tile_math(const _Float16* kr, const _Float16* vt
   // cleared, exact in FP16 for p in [2^-14, 2^8] -- and lo = p - hi (exact
   // in FP32, then rounded to FP16), so P.V carries ~21 bits of P.
   const float mb = safe_max(m);
-  f16x8 pb[2], pl[2];
 #pragma unroll
   for (int j = 0; j < 16; ++j) {
     const float pr = fast_exp2(__builtin_fmaf(sv[j], scale_log2, -mb));
@@ -513,6 +514,13 @@ __device__ __forceinline__ void tile_math(const _Float16* kr, const _Float16* vt
     pb[j >> 3][j & 7] = (_Float16)hi;
     pl[j >> 3][j & 7] = (_Float16)(pr - hi);
   }
+}
+
+template <int D>
+__device__ __forceinline__ void tile_pv(const _Float16* vtr, const f16x8 (&pb)[2],
+                                        const f16x8 (&pl)[2], f32x16 (&acc)[D / 32]) {
+  constexpr int DT = D / 32;
+  constexpr int VP = D + 16;
   // ---- O^T += V^T P^T; A operand tokens 16st + 8hf + 4g + k, dim lr ----
   // The MFMAs go round the DT accumulators, so consecutive ones are
   // independent.
@@ -632,9 +640,9 @@ __global__ __launch_bounds__(64 * W, 2) void tree_split_kernel(TreeParams P) {
   __shared__ __attribute__((aligned(16))) _Float16 s_stage[W * STAGE];
   // Q^T B operand of the row tile, held by every wave: lane (g, lr) holds
   // Q[row lr][16s + 8g .. +8] for each k-step s (rows past the tile's query
-  // rows: zeros).  The parent array in registers: lane i holds
-  // parent[i + 64c] (c < 4), so a wave walks ancestor chains with lane
-  // shuffles.  Both are loaded after tile 0's K/V (below).
+  // rows: row (node 0, head h), unused).  The parent array in registers:
+  // lane i holds parent[i + 64c] (c < 4), so a wave walks ancestor chains
+  // with lane shuffles.  Both are loaded between tile 0's K and V (below).
   uint4 qB[KS];
   static_assert(BC_MAX_TREE_NODES <= 256, "four parent registers per lane");
   int parr[4];
@@ -670,75 +678,106 @@ __global__ __launch_bounds__(64 * W, 2) void tree_split_kernel(TreeParams P) {
   // Issue the loads of this wave's tile `idx` from page ids ph.  Pages
   // outside the pool read page 0 and rows past the length read their page's
   // rows (all in bounds); both are masked.
-  auto issue = [&](int idx, const int (&ph)[2]) {
+  // K and V are issued apart (K first), so a wave can wait for K alone;
+  // draft_tag (std::true_type: a draft tile) picks the address form at
+  // compile time.
+  auto issue_half = [&](int idx, const int (&ph)[2], bool is_v, auto draft_tag) {
     const int it = tbeg + ln + LN * idx - ntd;  // prefix tile index when >= 0
-    rowok = 0;
+    uint4 (&dst)[KS] = is_v ? vreg : kreg;
+    if constexpr (!decltype(draft_tag)::value) {
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const bool okp = ph[q] >= 0 && ph[q] < P.phys_pages;
+        const size_t base = (size_t)(okp ? ph[q] : 0) * page_elems + (size_t)kvh * D;
+        const char* src = reinterpret_cast<const char*>((is_v ? P.v : P.k) + base);
+#pragma unroll
+        for (int j = 0; j < LPP; ++j) dst[q * LPP + j] = *reinterpret_cast<const uint4*>(src + loff[j]);
+      }
+    } else {
+      const uint16_t* src = is_v ? P.dv : P.dk;
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        const int dn = (it + ntd) * kTile + s * RPI + lrow;
+        const size_t off =
+            dn < P.nodes ? (((size_t)b * P.nodes + dn) * P.hkv + kvh) * D + lcol : lcol;
+        dst[s] = ldg16(src + off);
+      }
+    }
+  };
+  // Rows of the wave's tile `idx` that hold valid tokens (bit s: this
+  // lane's row of load s).
+  auto rows_of = [&](int idx, const int (&ph)[2]) {
+    const int it = tbeg + ln + LN * idx - ntd;
+    uint32_t ok = 0;
     if (it >= 0) {
       const int tb = it * kTile;
       const bool okp0 = ph[0] >= 0 && ph[0] < P.phys_pages;
       const bool okp1 = ph[1] >= 0 && ph[1] < P.phys_pages;
-      const bool whole = okp0 && okp1 && tb + kTile <= len;  // uniform: every row valid
-#pragma unroll
-      for (int q = 0; q < 2; ++q) {
-        const bool okp = q ? okp1 : okp0;
-        const size_t base = (size_t)(okp ? ph[q] : 0) * page_elems + (size_t)kvh * D;
-        const char* kb = reinterpret_cast<const char*>(P.k + base);
-        const char* vb = reinterpret_cast<const char*>(P.v + base);
-#pragma unroll
-        for (int j = 0; j < LPP; ++j) {
-          const int s = q * LPP + j;
-          kreg[s] = *reinterpret_cast<const uint4*>(kb + loff[j]);
-          vreg[s] = *reinterpret_cast<const uint4*>(vb + loff[j]);
-        }
-      }
-      if (whole) {
-        rowok = kAllRows;
-      } else {
-#pragma unroll
-        for (int s = 0; s < KS; ++s)
-          rowok |= (s < LPP ? okp0 : okp1) && tb + s * RPI + lrow < len ? 1u << s : 0u;
-      }
-    } else {
-#pragma unroll
-      for (int s = 0; s < KS; ++s) {
-        const int dn = (it + ntd) * kTile + s * RPI + lrow;
-        const bool ok = dn < P.nodes;
-        rowok |= ok ? 1u << s : 0u;
-        const size_t off = ok ? (((size_t)b * P.nodes + dn) * P.hkv + kvh) * D + lcol : lcol;
-        kreg[s] = ldg16(P.dk + off);
-        vreg[s] = ldg16(P.dv + off);
-      }
-    }
-  };
-
-  auto process = [&](int idx, const int (&ph)[2], const int (&next_ids)[2]) {
-    const int it = tbeg + ln + LN * idx;
-    const bool is_draft = it < ntd;
-    const int tbase = (is_draft ? it : it - ntd) * kTile;
-    // Valid token rows of the tile as a bit mask (bit i = token tbase + i):
-    // prefix tiles clip at the length and drop pages outside the pool;
-    // draft tiles take this row's ancestor-or-self set.
-    const uint32_t okbits =
-        is_draft ? ancestor_bits(parr, P.nodes, node, tbase)
-                 : prefix_bits(len - tbase, ph[0], ph[1], P.phys_pages);
-    // Stage K and V rows; rows that are not valid tokens may hold any bits
-    // (NaN included): their weight is zero, so their V row must be zero.
-#pragma unroll
-    for (int s = 0; s < KS; ++s) {
-      const int tl = s * RPI + lrow;
-      *reinterpret_cast<uint4*>(ks + tl * KP + lcol) = kreg[s];
-      *reinterpret_cast<uint4*>(vs + tl * VP + lcol) = vreg[s];
-    }
-    if (__builtin_amdgcn_ballot_w64(rowok != kAllRows)) {  // rows past the data: zero V
+      if (okp0 && okp1 && tb + kTile <= len) return kAllRows;  // uniform: every row valid
 #pragma unroll
       for (int s = 0; s < KS; ++s)
-        if (!((rowok >> s) & 1u))
-          *reinterpret_cast<uint4*>(vs + (s * RPI + lrow) * VP + lcol) = make_uint4(0, 0, 0, 0);
+        ok |= (s < LPP ? okp0 : okp1) && tb + s * RPI + lrow < len ? 1u << s : 0u;
+    } else {
+#pragma unroll
+      for (int s = 0; s < KS; ++s)
+        ok |= (it + ntd) * kTile + s * RPI + lrow < P.nodes ? 1u << s : 0u;
     }
+    return ok;
+  };
+  auto issue = [&](int idx, const int (&ph)[2]) {
+    if (tbeg + ln + LN * idx < ntd) {
+      issue_half(idx, ph, false, std::true_type{});
+      issue_half(idx, ph, true, std::true_type{});
+    } else {
+      issue_half(idx, ph, false, std::false_type{});
+      issue_half(idx, ph, true, std::false_type{});
+    }
+    rowok = rows_of(idx, ph);
+  };
+
+  // first_tag: std::true_type for the wave's first tile (a separate copy
+  // of the tile code), std::false_type for the rest.
+  // Valid token rows of tile idx as a bit mask (bit i = token tbase + i):
+  // prefix tiles clip at the length and drop pages outside the pool; draft
+  // tiles take this row's ancestor-or-self set.
+  auto okbits_of = [&](int idx, const int (&ph)[2], bool is_draft) {
+    const int it = tbeg + ln + LN * idx;
+    const int tbase = (is_draft ? it : it - ntd) * kTile;
+    return is_draft ? ancestor_bits(parr, P.nodes, node, tbase)
+                    : prefix_bits(len - tbase, ph[0], ph[1], P.phys_pages);
+  };
+  auto process = [&](int idx, uint32_t okbits, const int (&next_ids)[2], auto first_tag) {
+    // Stage K and V rows; rows that are not valid tokens may hold any bits
+    // (NaN included): their weight is zero, so their V row must be zero.
+    auto stage_v = [&]() {
+#pragma unroll
+      for (int s = 0; s < KS; ++s)
+        *reinterpret_cast<uint4*>(vs + (s * RPI + lrow) * VP + lcol) = vreg[s];
+      if (__builtin_amdgcn_ballot_w64(rowok != kAllRows)) {  // rows past the data: zero V
+#pragma unroll
+        for (int s = 0; s < KS; ++s)
+          if (!((rowok >> s) & 1u))
+            *reinterpret_cast<uint4*>(vs + (s * RPI + lrow) * VP + lcol) = make_uint4(0, 0, 0, 0);
+      }
+    };
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+      *reinterpret_cast<uint4*>(ks + (s * RPI + lrow) * KP + lcol) = kreg[s];
+    // The first tile's scores start as soon as its K is staged (its V was
+    // issued after K and Q); later tiles stage both, then issue the next
+    // tile's loads, which are then in flight during this tile's MFMAs.
+    constexpr bool first = decltype(first_tag)::value;
+    if (!first) stage_v();
     wave_lds_sync();
-    // The rows are in LDS: the next tile's loads go out now.
-    if (idx + 1 < nmine) issue(idx + 1, next_ids);
-    tile_math<D>(ks + lr * KP, vtr, qB, okbits, P.scale_log2, g, acc, m, l);
+    if (!first && idx + 1 < nmine) issue(idx + 1, next_ids);
+    f16x8 pb[2], pl[2];
+    tile_scores<D>(ks + lr * KP, qB, okbits, P.scale_log2, g, acc, m, l, pb, pl);
+    if constexpr (first) {
+      stage_v();
+      wave_lds_sync();
+      if (idx + 1 < nmine) issue(idx + 1, next_ids);
+    }
+    tile_pv<D>(vtr, pb, pl, acc);
     // The staging area is rewritten by the next tile.
     wave_lds_sync();
   };
@@ -751,28 +790,52 @@ __global__ __launch_bounds__(64 * W, 2) void tree_split_kernel(TreeParams P) {
     ph[0] = __builtin_amdgcn_readlane(idv, 2 * (idx & 31));
     ph[1] = __builtin_amdgcn_readlane(idv, 2 * (idx & 31) + 1);
   };
-  if (nmine > 0) issue(0, cur);
-  // Q and the parents load without branches (clamped addresses, then
-  // selects), so the first tile's waits need not cover them.
-  {
-    const uint16_t* qp = P.dq + (((size_t)b * P.nodes + node) * P.hq + h) * D + 8 * g;
+  // Load order: tile 0's K, then Q and the parents, then tile 0's V, so the
+  // first scores wait for K, Q and the parents only.  Q and the parents
+  // load without branches or selects (a select right after a load would
+  // wait for it there): lanes past the tile's query rows read row (node 0,
+  // head h), whose scores land in columns that are never written out, and
+  // parent entries past the node count repeat the last one and are never
+  // read (walks visit nodes in [0, nodes) only).  Tile 0's loads go out
+  // even for a wave without tiles (its addresses stay inside the tensors),
+  // so every path issues the same loads and the compiler's wait counts for
+  // Q and the parents need not cover V.
+  // The start, up to the first tile's scores, is compiled once for a first
+  // tile of draft rows and once for one of prefix rows: a branch between
+  // the loads and their waits would make the compiler's wait counts assume
+  // the fewest loads either side issued, so the waits for Q would also wait
+  // for V.
+  auto start = [&](auto draft_tag) {
+    constexpr bool DRAFT = decltype(draft_tag)::value;
+    issue_half(0, cur, false, draft_tag);
+    {
+      const uint16_t* qp = P.dq + (((size_t)b * P.nodes + node) * P.hq + h) * D + 8 * g;
 #pragma unroll
-    for (int s = 0; s < KS; ++s) qB[s] = ldg16(qp + 16 * s);
+      for (int s = 0; s < KS; ++s) qB[s] = ldg16(qp + 16 * s);
+    }
 #pragma unroll
-    for (int s = 0; s < KS; ++s) qB[s] = rvalid ? qB[s] : make_uint4(0, 0, 0, 0);
-  }
-#pragma unroll
-  for (int c = 0; c < 4; ++c) {
-    const int i = lane + 64 * c;
-    parr[c] = P.parent[(size_t)b * P.nodes + min(i, P.nodes - 1)];
-    parr[c] = i < P.nodes ? parr[c] : -1;
-  }
+    for (int c = 0; c < 4; ++c)
+      parr[c] = P.parent[(size_t)b * P.nodes + min(lane + 64 * c, P.nodes - 1)];
+    issue_half(0, cur, true, draft_tag);
+    rowok = rows_of(0, cur);
+    if (nmine > 0) {
+      int nxt[2] = {-1, -1};
+      if (1 < nmine) ids_of(1, nxt);
+      process(0, okbits_of(0, cur, DRAFT), nxt, std::true_type{});
+      cur[0] = nxt[0];
+      cur[1] = nxt[1];
+    }
+  };
+  if (tbeg + ln < ntd)
+    start(std::true_type{});
+  else
+    start(std::false_type{});
   // The loads run one tile ahead of the MFMAs: while tile idx is processed,
   // tile idx+1's rows are loading.
-  for (int idx = 0; idx < nmine; ++idx) {
+  for (int idx = 1; idx < nmine; ++idx) {
     int nxt[2] = {-1, -1};
     if (idx + 1 < nmine) ids_of(idx + 1, nxt);
-    process(idx, cur, nxt);
+    process(idx, okbits_of(idx, cur, tbeg + ln + LN * idx < ntd), nxt, std::false_type{});
     cur[0] = nxt[0];
     cur[1] = nxt[1];
   }
