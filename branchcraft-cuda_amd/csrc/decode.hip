@@ -295,9 +295,10 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == kMaxWaves ? 3 : 2) void paged_
       (long long)kvh * P.head_stride + (long long)lrow * P.slot_stride + lcol;
   const long long row_step = (long long)RPI * P.slot_stride;
 
-  // Issue cursor: walks the same pages ahead of the compute cursor.  Page
-  // ids are scalar loads (counted by lgkmcnt, not vmcnt), fetched one step
-  // before the K/V loads that use them.  Issues past the range still load
+  // Issue cursor: walks the same pages ahead of the compute cursor.  The
+  // cursor is the same in every lane, but the compiler keeps it in vector
+  // registers, so page ids are vector loads counted by vmcnt like the K/V
+  // loads; the loops below order them accordingly.  Issues past the range still load
   // (every path keeps the same loads in flight), but from page 0 of the pool
   // like an out-of-pool id: all of them share that one L2-resident page,
   // whereas repeating the range's last page would fetch it from HBM again,

@@ -198,7 +198,7 @@ int bc_packed_decode(bc_shape shape, const bc_half* q, const bc_half* packed_kv,
 size_t bc_packed_decode_workspace_size(bc_shape shape);
 
 /* bc_packed_decode with the batch's pages spread over equal ranges of the
- * concatenated sequences, two workgroups per CU, and an FP32 merge of the
+ * concatenated sequences, one workgroup per CU, and an FP32 merge of the
  * sequences a range boundary cuts.  The workgroup count and the workspace
  * size depend on the shape and the device's CU count only; the kernels find
  * the ranges from the lengths on the device, so no lengths are read on the
