@@ -460,10 +460,11 @@ __device__ __forceinline__ uint32_t ancestor_bits(const int (&parr)[4], int node
 // chain over the k-steps and the masked online-softmax update of (m, l,
 // acc), leaving P as an FP16 hi/lo pair; tile_pv: O^T += V^T P^T.  kr is
 // this lane's K row (token lr), vtr its transpose-read address in the V
-// rows, qB the Q^T B operand and okbits the valid tokens of the lane's
-// query row.
-template <int D>
-__device__ __forceinline__ void tile_scores(const _Float16* kr, const uint4 (&qB)[D / 16],
+// rows, qf this lane's Q^T B-operand fragments (k-step s at qf[QS s]: in
+// LDS, QS = 64; in registers, QS = 1) and okbits the valid tokens of the
+// lane's query row.
+template <int D, int QS>
+__device__ __forceinline__ void tile_scores(const _Float16* kr, const uint4* qf,
                                             uint32_t okbits, float scale_log2, int g,
                                             f32x16 (&acc)[D / 32], float& m, float& l,
                                             f16x8 (&pb)[2], f16x8 (&pl)[2]) {
@@ -475,7 +476,7 @@ __device__ __forceinline__ void tile_scores(const _Float16* kr, const uint4 (&qB
 #pragma unroll
   for (int s = 0; s < KS; ++s) {
     const uint4 k0 = *reinterpret_cast<const uint4*>(kr + 16 * s + 8 * g);
-    sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_f16x8(k0), as_f16x8(qB[s]), sc, 0, 0, 0);
+    sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_f16x8(k0), as_f16x8(qf[QS * s]), sc, 0, 0, 0);
   }
   // sc[j] holds token row 8*(j/4) + 4*g + j%4.  Scores stay unscaled here;
   // the scale enters the running max once and the exp2 argument as an FMA.
@@ -638,12 +639,17 @@ __global__ __launch_bounds__(64 * W, 2) void tree_split_kernel(TreeParams P) {
   const int h = kvh * P.group + (rvalid ? r % P.group : 0);
 
   __shared__ __attribute__((aligned(16))) _Float16 s_stage[W * STAGE];
-  // Q^T B operand of the row tile, held by every wave: lane (g, lr) holds
-  // Q[row lr][16s + 8g .. +8] for each k-step s (rows past the tile's query
-  // rows: row (node 0, head h), unused).  The parent array in registers:
-  // lane i holds parent[i + 64c] (c < 4), so a wave walks ancestor chains
-  // with lane shuffles.  Both are loaded between tile 0's K and V (below).
-  uint4 qB[KS];
+  // Q^T B operand of each request's row tile: lane (g, lr) of k-step s
+  // holds Q[row lr][16s + 8g .. +8] (rows past the tile's query rows: row
+  // (node 0, head h), unused).  It stays in LDS for the whole kernel (read
+  // back per tile, which keeps 32 registers free), except in the D = 64
+  // two-request workgroups, where it would leave room for one workgroup per
+  // CU instead of two: there every wave holds it in registers.  The parent
+  // array in registers: lane i holds parent[i + 64c] (c < 4), so a wave
+  // walks ancestor chains with lane shuffles.
+  constexpr bool QL = !(D == 64 && RQ == 2);
+  __shared__ uint4 s_q[QL ? RQ * KS * 64 : 1];
+  uint4 qreg[QL ? 1 : KS];
   static_assert(BC_MAX_TREE_NODES <= 256, "four parent registers per lane");
   int parr[4];
 
@@ -771,7 +777,11 @@ __global__ __launch_bounds__(64 * W, 2) void tree_split_kernel(TreeParams P) {
     wave_lds_sync();
     if (!first && idx + 1 < nmine) issue(idx + 1, next_ids);
     f16x8 pb[2], pl[2];
-    tile_scores<D>(ks + lr * KP, qB, okbits, P.scale_log2, g, acc, m, l, pb, pl);
+    if constexpr (QL)
+      tile_scores<D, 64>(ks + lr * KP, s_q + (size_t)rq * KS * 64 + lane, okbits,
+                         P.scale_log2, g, acc, m, l, pb, pl);
+    else
+      tile_scores<D, 1>(ks + lr * KP, qreg, okbits, P.scale_log2, g, acc, m, l, pb, pl);
     if constexpr (first) {
       stage_v();
       wave_lds_sync();
@@ -790,46 +800,79 @@ __global__ __launch_bounds__(64 * W, 2) void tree_split_kernel(TreeParams P) {
     ph[0] = __builtin_amdgcn_readlane(idv, 2 * (idx & 31));
     ph[1] = __builtin_amdgcn_readlane(idv, 2 * (idx & 31) + 1);
   };
-  // Load order: tile 0's K, then Q and the parents, then tile 0's V, so the
-  // first scores wait for K, Q and the parents only.  Q and the parents
-  // load without branches or selects (a select right after a load would
-  // wait for it there): lanes past the tile's query rows read row (node 0,
-  // head h), whose scores land in columns that are never written out, and
-  // parent entries past the node count repeat the last one and are never
-  // read (walks visit nodes in [0, nodes) only).  Tile 0's loads go out
-  // even for a wave without tiles (its addresses stay inside the tensors),
-  // so every path issues the same loads and the compiler's wait counts for
-  // Q and the parents need not cover V.
-  // The start, up to the first tile's scores, is compiled once for a first
-  // tile of draft rows and once for one of prefix rows: a branch between
-  // the loads and their waits would make the compiler's wait counts assume
-  // the fewest loads either side issued, so the waits for Q would also wait
-  // for V.
-  auto start = [&](auto draft_tag) {
-    constexpr bool DRAFT = decltype(draft_tag)::value;
-    issue_half(0, cur, false, draft_tag);
-    {
-      const uint16_t* qp = P.dq + (((size_t)b * P.nodes + node) * P.hq + h) * D + 8 * g;
+  // Tile 0's loads as one straight-line sequence for a draft and a prefix
+  // first tile alike (each load's address is selected per lane): after a
+  // branch with loads on both sides, the compiler's wait counts assume the
+  // fewest loads either side issued, so later waits would cover loads they
+  // need not wait for.  Pages outside the pool read page 0 and draft rows
+  // past the node count read row 0 (all in bounds); both are masked.
+  auto issue_first = [&](const int (&ph)[2], bool is_v) {
+    const int it = tbeg + ln - ntd;  // prefix tile index when >= 0
+    uint4 (&dst)[KS] = is_v ? vreg : kreg;
+    const uint16_t* pbase = is_v ? P.v : P.k;
+    const uint16_t* dbase = is_v ? P.dv : P.dk;
+    // Draft row of load s: dn0 + s * RPI, each RPI rows dstep elements on.
+    const int dn0 = (it + ntd) * kTile + lrow;
+    const size_t dstep = (size_t)RPI * P.hkv * D;
+    const uint16_t* d0 = dbase + (((size_t)b * P.nodes + dn0) * P.hkv + kvh) * D + lcol;
 #pragma unroll
-      for (int s = 0; s < KS; ++s) qB[s] = ldg16(qp + 16 * s);
-    }
+    for (int q = 0; q < 2; ++q) {
+      const bool okp = ph[q] >= 0 && ph[q] < P.phys_pages;
+      const char* pg = reinterpret_cast<const char*>(
+          pbase + (size_t)(okp ? ph[q] : 0) * page_elems + (size_t)kvh * D);
 #pragma unroll
-    for (int c = 0; c < 4; ++c)
-      parr[c] = P.parent[(size_t)b * P.nodes + min(lane + 64 * c, P.nodes - 1)];
-    issue_half(0, cur, true, draft_tag);
-    rowok = rows_of(0, cur);
-    if (nmine > 0) {
-      int nxt[2] = {-1, -1};
-      if (1 < nmine) ids_of(1, nxt);
-      process(0, okbits_of(0, cur, DRAFT), nxt, std::true_type{});
-      cur[0] = nxt[0];
-      cur[1] = nxt[1];
+      for (int j = 0; j < LPP; ++j) {
+        const int s = q * LPP + j;
+        const uint16_t* da = dn0 + s * RPI < P.nodes ? d0 + s * dstep : dbase + lcol;
+        const uint4* src = it >= 0 ? reinterpret_cast<const uint4*>(pg + loff[j])
+                                   : reinterpret_cast<const uint4*>(da);
+        dst[s] = *src;
+      }
     }
   };
-  if (tbeg + ln < ntd)
-    start(std::true_type{});
-  else
-    start(std::false_type{});
+  // Load order: this wave's share of Q, tile 0's K, the parents, tile 0's V,
+  // so the first scores wait for Q, K and the parents only.  A wave without
+  // tiles issues tile 0's loads too (its addresses stay inside the tensors),
+  // so every wave runs the same loads and barriers.  Q and the parents load
+  // without selects (a select right after a load would wait for it there):
+  // lanes past the tile's query rows read row (node 0, head h), whose scores
+  // land in columns that are never written out, and parent entries past the
+  // node count repeat the last one and are never read (walks visit nodes in
+  // [0, nodes) only).
+  //
+  // Q^T fragments: with Q in LDS, the LN waves of a request load KS / LN of
+  // them each into s_q, so the workgroup fetches each fragment once instead
+  // of once per wave (every wave of a request reads the same rows).
+  constexpr int QPW = QL ? (KS + LN - 1) / LN : KS;  // fragments loaded per wave
+  uint4 qown[QPW];
+  {
+    const uint16_t* qp = P.dq + (((size_t)b * P.nodes + node) * P.hq + h) * D + 8 * g;
+#pragma unroll
+    for (int j = 0; j < QPW; ++j)
+      qown[j] = ldg16(qp + 16 * (QL ? min(ln + LN * j, KS - 1) : j));
+  }
+  issue_first(cur, false);
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+    parr[c] = P.parent[(size_t)b * P.nodes + min(lane + 64 * c, P.nodes - 1)];
+  issue_first(cur, true);
+  rowok = rows_of(0, cur);
+  if constexpr (QL) {
+#pragma unroll
+    for (int j = 0; j < QPW; ++j)
+      if (ln + LN * j < KS) s_q[((size_t)rq * KS + ln + LN * j) * 64 + lane] = qown[j];
+    __syncthreads();  // every wave's Q fragments are in s_q
+  } else {
+#pragma unroll
+    for (int j = 0; j < KS; ++j) qreg[j] = qown[j];
+  }
+  if (nmine > 0) {
+    int nxt[2] = {-1, -1};
+    if (1 < nmine) ids_of(1, nxt);
+    process(0, okbits_of(0, cur, tbeg + ln < ntd), nxt, std::true_type{});
+    cur[0] = nxt[0];
+    cur[1] = nxt[1];
+  }
   // The loads run one tile ahead of the MFMAs: while tile idx is processed,
   // tile idx+1's rows are loading.
   for (int idx = 1; idx < nmine; ++idx) {
@@ -846,9 +889,10 @@ __global__ __launch_bounds__(64 * W, 2) void tree_split_kernel(TreeParams P) {
   // LN states of its request's share of the tile (row mrow, DPT dims) and
   // writes it.
   constexpr int XP = D + 4;  // padded rows: a float4 access spreads over banks
-  static_assert(W * STAGE * 2 >= W * 32 * XP * 4, "merge buffer fits");
+  static_assert(W * STAGE * 2 >= W * 32 * (XP + 2) * 4, "merge buffers fit");
   float* xacc = reinterpret_cast<float*>(s_stage);  // [W][32 rows][XP]
-  __shared__ float s_ml[W][32][2];
+  // (max, sum) per wave and row, after the accumulators
+  auto s_ml = reinterpret_cast<float(*)[32][2]>(xacc + (size_t)W * 32 * XP);
   __syncthreads();  // the staging areas are reused below
   {
     float* dst = xacc + (size_t)wave * 32 * XP + (size_t)lr * XP;
