@@ -555,20 +555,22 @@ __device__ __forceinline__ void wave_lds_sync() {
 }
 
 // Split tree verification.  Unit = (request, KV head, row tile); its work is
-// one tile space: prefix tiles [0, ntp) (32 tokens each, up to the request's
-// length) followed by the draft tiles.  Workgroup `part` of a unit takes
-// tiles [part*T, part*T + T), T = P.tiles_per_part, and its W waves take
-// those tiles round-robin.  A wave loads a tile's K and V as whole token
-// rows (each 16-byte load instruction covers complete 128-byte lines:
-// measured 2x the tile rate of loading K in the MFMA operand layout, where
-// an instruction touches 32 rows), stages them in its own LDS area -- K
-// rows at a pitch for conflict-free A-operand reads, V rows at a pitch for
-// transpose reads -- and issues the next tile's loads as soon as the rows
-// are staged, so they are in flight during the current tile's MFMAs.
-// Masks, softmax and the hi/lo P.V product are tree_kernel's.  The waves
-// merge through LDS; with one part per unit (no workspace) wave 0 writes the
-// output, otherwise every part with tiles writes an FP32 partial per row,
-// slot (row, part), and merge_split_kernel combines them.
+// one tile space: the draft tiles [0, ntd) followed by the prefix tiles (32
+// tokens each, up to the request's length).  Workgroup `part` of a unit
+// takes tiles [part*T, part*T + T), T = P.tiles_per_part, and its W waves
+// take those tiles round-robin.  The row tile's Q^T fragments are fetched
+// once per workgroup into LDS, where the score MFMAs read them.  A wave
+// loads a tile's K and V as whole token rows (each 16-byte load instruction
+// covers complete 128-byte lines: measured 2x the tile rate of loading K in
+// the MFMA operand layout, where an instruction touches 32 rows), stages
+// them in its own LDS area -- K rows at a pitch for conflict-free A-operand
+// reads, V rows at a pitch for transpose reads -- and issues the next tile's
+// loads as soon as the rows are staged, so they are in flight during the
+// current tile's MFMAs.  Masks, softmax and the hi/lo P.V product are
+// tree_kernel's.  The waves merge through LDS; with one part per unit (no
+// workspace) wave 0 writes the output, otherwise every part with tiles
+// writes an FP32 partial per row, slot (row, part), and merge_split_kernel
+// combines them.
 template <int D, int W, int RQ>
 __global__ __launch_bounds__(64 * W, 2) void tree_split_kernel(TreeParams P) {
   constexpr int KS = D / 16;      // MFMA k-steps; also load instructions per tile
