@@ -463,7 +463,10 @@ __device__ __forceinline__ uint32_t ancestor_bits(const int (&parr)[4], int node
 // rows, qf this lane's Q^T B-operand fragments (k-step s at qf[QS s]: in
 // LDS, QS = 64; in registers, QS = 1) and okbits the valid tokens of the
 // lane's query row.
-template <int D, int QS>
+// FIRST: the wave's first tile; its running max starts at -inf and acc is
+// not yet defined, so the rescale is skipped (tile_pv then starts acc from
+// zero).
+template <int D, int QS, bool FIRST>
 __device__ __forceinline__ void tile_scores(const _Float16* kr, const uint4* qf,
                                             uint32_t okbits, float scale_log2, int g,
                                             f32x16 (&acc)[D / 32], float& m, float& l,
@@ -493,15 +496,19 @@ __device__ __forceinline__ void tile_scores(const _Float16* kr, const uint4* qf,
 #pragma unroll
   for (int j = 0; j < 16; ++j) tmax = __builtin_fmaxf(tmax, sv[j]);
   tmax = __builtin_fmaxf(tmax, shfl_xor_f(tmax, 32)) * scale_log2;
-  const float mnew = __builtin_fmaxf(m, tmax);
-  if (__builtin_amdgcn_ballot_w64(mnew > m + kRescaleSlack)) {
-    const float alpha = fast_exp2(m - safe_max(mnew));
-    l *= alpha;
+  if constexpr (FIRST) {
+    m = tmax;  // l is still 0
+  } else {
+    const float mnew = __builtin_fmaxf(m, tmax);
+    if (__builtin_amdgcn_ballot_w64(mnew > m + kRescaleSlack)) {
+      const float alpha = fast_exp2(m - safe_max(mnew));
+      l *= alpha;
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
+      for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-      for (int j = 0; j < 16; ++j) acc[dt][j] *= alpha;
-    m = mnew;
+        for (int j = 0; j < 16; ++j) acc[dt][j] *= alpha;
+      m = mnew;
+    }
   }
   // P splits into an FP16 hi part -- p with the low 13 mantissa bits
   // cleared, exact in FP16 for p in [2^-14, 2^8] -- and lo = p - hi (exact
@@ -517,7 +524,9 @@ __device__ __forceinline__ void tile_scores(const _Float16* kr, const uint4* qf,
   }
 }
 
-template <int D>
+// FIRST: acc starts from zero (the first MFMA of each accumulator takes a
+// zero C operand).
+template <int D, bool FIRST>
 __device__ __forceinline__ void tile_pv(const _Float16* vtr, const f16x8 (&pb)[2],
                                         const f16x8 (&pl)[2], f32x16 (&acc)[D / 32]) {
   constexpr int DT = D / 32;
@@ -534,11 +543,14 @@ __device__ __forceinline__ void tile_pv(const _Float16* vtr, const f16x8 (&pb)[2
       const f16x4 hi = lds_read_tr(vtr + (16 * st + 8) * VP + 32 * dt);
       av[dt][st] = f16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
     }
+  const f32x16 zero = {};
 #pragma unroll
   for (int st = 0; st < 2; ++st)
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
-      acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[dt][st], pb[st], acc[dt], 0, 0, 0);
+      acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[dt][st], pb[st],
+                                                       FIRST && st == 0 ? zero : acc[dt], 0, 0,
+                                                       0);
 #pragma unroll
   for (int st = 0; st < 2; ++st)
 #pragma unroll
@@ -664,11 +676,7 @@ __global__ __launch_bounds__(64 * W, 2) void tree_split_kernel(TreeParams P) {
   const int lrow = lane / LPR, lcol = 8 * (lane % LPR);
   const size_t tok_stride = (size_t)P.hkv * D;
 
-  f32x16 acc[DT];
-#pragma unroll
-  for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-    for (int j = 0; j < 16; ++j) acc[dt][j] = 0.f;
+  f32x16 acc[DT];  // defined by the first tile, or zeroed for a wave without tiles
   float m = kNegInf, l = 0.f;
 
   uint4 kreg[KS], vreg[KS];
@@ -780,16 +788,16 @@ __global__ __launch_bounds__(64 * W, 2) void tree_split_kernel(TreeParams P) {
     if (!first && idx + 1 < nmine) issue(idx + 1, next_ids);
     f16x8 pb[2], pl[2];
     if constexpr (QL)
-      tile_scores<D, 64>(ks + lr * KP, s_q + (size_t)rq * KS * 64 + lane, okbits,
-                         P.scale_log2, g, acc, m, l, pb, pl);
+      tile_scores<D, 64, first>(ks + lr * KP, s_q + (size_t)rq * KS * 64 + lane, okbits,
+                                P.scale_log2, g, acc, m, l, pb, pl);
     else
-      tile_scores<D, 1>(ks + lr * KP, qreg, okbits, P.scale_log2, g, acc, m, l, pb, pl);
+      tile_scores<D, 1, first>(ks + lr * KP, qreg, okbits, P.scale_log2, g, acc, m, l, pb, pl);
     if constexpr (first) {
       stage_v();
       wave_lds_sync();
       if (idx + 1 < nmine) issue(idx + 1, next_ids);
     }
-    tile_pv<D>(vtr, pb, pl, acc);
+    tile_pv<D, first>(vtr, pb, pl, acc);
     // The staging area is rewritten by the next tile.
     wave_lds_sync();
   };
@@ -874,6 +882,11 @@ __global__ __launch_bounds__(64 * W, 2) void tree_split_kernel(TreeParams P) {
     process(0, okbits_of(0, cur, tbeg + ln < ntd), nxt, std::true_type{});
     cur[0] = nxt[0];
     cur[1] = nxt[1];
+  } else {
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) acc[dt][j] = 0.f;
   }
   // The loads run one tile ahead of the MFMAs: while tile idx is processed,
   // tile idx+1's rows are loading.
