@@ -71,7 +71,17 @@ struct TreeParams {
   // tree_split_kernel: parts per unit and tiles per part; with parts > 1,
   // part_acc/part_ml hold P.parts slots per output row.
   int parts, tiles_per_part;
+  // ceil(2^32 / d) for d = group and d = row_tiles (0: divide plainly), and
+  // whether the launch is a (KV head x row tile, request group, part) grid.
+  unsigned long long group_mul, rt_mul;
+  int grid3d;
 };
+
+// n / d, as a multiply-high when the host passed mul = ceil(2^32 / d) (exact
+// for n * d < 2^32, which the host checks), else a plain division.
+__device__ __forceinline__ int div_by(int n, int d, unsigned long long mul) {
+  return mul ? (int)(((unsigned long long)(unsigned)n * mul) >> 32) : n / d;
+}
 
 __device__ __forceinline__ f16x8 as_f16x8(const uint4 u) {
   return __builtin_bit_cast(f16x8, u);
@@ -605,16 +615,25 @@ __global__ __launch_bounds__(64 * W, 2) void tree_split_kernel(TreeParams P) {
   // tiles at the same time (their shared pages then meet in the CU's L1).
   const int rq = wave / LN;
   const int ln = wave % LN;
-  const int zdim = P.hkv * P.row_tiles;
-  const int units = zdim * ((P.batch + RQ - 1) / RQ);
-  const int unit = blockIdx.x % units;  // (KV head, row tile) in the low bits
-  const int part = blockIdx.x / units;
-  const int z = unit % zdim;
-  const int b0 = (unit / zdim) * RQ;
+  // Workgroup ids put (KV head, row tile) in the low bits, then the request
+  // group, then the part (a 3-D grid, or the same order flattened).
+  int z, b0, part;
+  if (P.grid3d) {
+    z = blockIdx.x;
+    b0 = blockIdx.y * RQ;
+    part = blockIdx.z;
+  } else {
+    const int zdim = P.hkv * P.row_tiles;
+    const int units = zdim * ((P.batch + RQ - 1) / RQ);
+    const int unit = blockIdx.x % units;
+    part = blockIdx.x / units;
+    z = unit % zdim;
+    b0 = (unit / zdim) * RQ;
+  }
   const bool present = b0 + rq < P.batch;  // uniform per wave
   const int b = present ? b0 + rq : b0;    // absent waves read request b0, unused
-  const int kvh = z / P.row_tiles;
-  const int rt = z % P.row_tiles;
+  const int kvh = div_by(z, P.row_tiles, P.rt_mul);
+  const int rt = z - kvh * P.row_tiles;
   const int T = P.tiles_per_part;
   const int tbeg = part * T;
 
@@ -649,8 +668,9 @@ __global__ __launch_bounds__(64 * W, 2) void tree_split_kernel(TreeParams P) {
 
   const int r = rt * 32 + lr;
   const bool rvalid = r < P.rows;
-  const int node = rvalid ? r / P.group : 0;
-  const int h = kvh * P.group + (rvalid ? r % P.group : 0);
+  const int rnode = div_by(r, P.group, P.group_mul);
+  const int node = rvalid ? rnode : 0;
+  const int h = kvh * P.group + (rvalid ? r - rnode * P.group : 0);
 
   __shared__ __attribute__((aligned(16))) _Float16 s_stage[W * STAGE];
   // Q^T B operand of each request's row tile: lane (g, lr) of k-step s
@@ -957,7 +977,9 @@ __global__ __launch_bounds__(64 * W, 2) void tree_split_kernel(TreeParams P) {
       o[j + 3] += wt * v4.w;
     }
   }
-  const size_t orow = ((size_t)b * P.nodes + rr / P.group) * P.hq + kvh * P.group + rr % P.group;
+  const int rrn = div_by(rr, P.group, P.group_mul);
+  const size_t orow =
+      ((size_t)b * P.nodes + rrn) * P.hq + kvh * P.group + (rr - rrn * P.group);
   if (P.parts == 1) {
     const float inv = 1.f / ll;  // every row sees its own node: ll > 0
     float* dst = P.out + orow * D + md0;
@@ -1331,6 +1353,14 @@ TreeParams make_params(const bc_shape& s, const bc_tree_inputs& in, int nodes) {
   P.rows = nodes * P.group;
   P.row_tiles = (P.rows + 31) / 32;
   P.scale_log2 = (float)(1.4426950408889634 / __builtin_sqrt((double)s.dim));
+  // Multiply-high division needs n * d < 2^32 for every n it divides: row
+  // indices stay below 32 * row_tiles, (KV head, row tile) indices below
+  // hkv * row_tiles.
+  const unsigned long long lim = 1ull << 32;
+  if ((unsigned long long)P.row_tiles * 32 * P.group < lim)
+    P.group_mul = (lim + P.group - 1) / P.group;
+  if ((unsigned long long)P.hkv * P.row_tiles * P.row_tiles < lim)
+    P.rt_mul = (lim + P.row_tiles - 1) / P.row_tiles;
   return P;
 }
 
@@ -1485,7 +1515,10 @@ hipError_t launch_split(TreeParams& P, int dim, const SplitPlan& plan, void* wor
     P.part_ml = reinterpret_cast<float*>(static_cast<char*>(workspace) + acc_bytes);
   }
   const size_t groups = ((size_t)P.batch + plan.rq - 1) / plan.rq;
-  const dim3 grid((unsigned)((size_t)plan.parts * groups * P.hkv * P.row_tiles));
+  P.grid3d = groups <= 65535;
+  const dim3 grid = P.grid3d
+      ? dim3((unsigned)(P.hkv * P.row_tiles), (unsigned)groups, (unsigned)plan.parts)
+      : dim3((unsigned)((size_t)plan.parts * groups * P.hkv * P.row_tiles));
   if (dim == 64) launch_split_kernel<64>(P, plan, grid, st);
   else launch_split_kernel<128>(P, plan, grid, st);
   hipError_t err = hipGetLastError();
