@@ -1468,12 +1468,11 @@ SplitPlan split_plan(const bc_shape& s, int nodes, int cus) {
   };
   const long long u = units > 0 ? units : 1;
   // A single pass whose eight waves take two tiles or fewer each beats a
-  // split, which adds the merge launch, once its units fill an eighth of the
-  // CUs (8 requests x 256 tokens: 10.1 against 10.7 us; 16 x 256: 10.3
-  // against 13.2 us); one request over 256 or 384 tokens splits as fast or
-  // faster (9.5 against 10.2 us at 384).
-  if (max_tiles <= 2 * 8 && 8 * u >= cus)
-    return pair_requests(s.batch, u, SplitPlan{1, max_tiles, 8}, cus);
+  // split, which adds the merge launch (one request over 256 tokens: 8.2
+  // against 9.6 us, over 384: 8.4 against 9.3 us; 2 x 256: 8.5 against
+  // 9.6 us; 16 x 256: 10.3 against 13.2 us).  With three tiles per wave the
+  // split wins (one request over 512 tokens: 9.1 against 9.7 us).
+  if (max_tiles <= 2 * 8) return pair_requests(s.batch, u, SplitPlan{1, max_tiles, 8}, cus);
   const SplitPlan eight = plan_for(8, cus / u);
   const SplitPlan four = plan_for(4, 2LL * cus / u);
   // Waves with at least one tile, and CUs with a workgroup.

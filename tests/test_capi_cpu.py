@@ -232,14 +232,12 @@ def test_workspace_sizes():
         size = lib.bc_tree_verify_workspace_size(capi.Shape(batch, 32, 8, 128, 129, 160), 7)
         assert (size > 0) == split, batch
     # Prefixes short enough that a single pass gives each of its eight waves
-    # two tiles or fewer (16 tiles, drafts included) do not split once the
-    # units (request, KV head, row tile) fill an eighth of the CUs.
-    for batch in (4, 8):
+    # two tiles or fewer (16 tiles, drafts included) do not split.
+    for batch in (1, 2, 4, 8):
         short = capi.Shape(batch, 32, 8, 128, 30, 160)  # 480 tokens + 1 draft tile
         assert lib.bc_tree_verify_workspace_size(short, 7) == 0
         longer = capi.Shape(batch, 32, 8, 128, 31, 160)  # 496 tokens: 17 tiles
         assert lib.bc_tree_verify_workspace_size(longer, 7) > 0
-    assert lib.bc_tree_verify_workspace_size(capi.Shape(1, 32, 8, 128, 16, 160), 7) > 0
 
 
 def test_torch_ops_register_reference_schemas():
