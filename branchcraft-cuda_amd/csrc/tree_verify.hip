@@ -1000,14 +1000,16 @@ __global__ __launch_bounds__(64 * W, 2) void tree_split_kernel(TreeParams P) {
 // Combines tree_split_kernel's partials: one wave per output row (b, node,
 // h); the parts that held tiles, [0, nparts) with nparts from the request's
 // length, wrote slots (row, part).  Lane p holds slot p's (max, sum); the
-// weights are formed once and every lane accumulates its dims from eight
-// slots per step, all loads of a step issued before the first use.  The
-// (max, sum) loads and the first step's accumulators go out together with
-// the length, and slots past nparts are masked afterwards (their contents
-// are whatever the workspace held).
-template <int D>
+// weights are formed once and every lane accumulates its dims from the
+// slots.  The (max, sum) loads and the first 8 * NB slots' accumulators go
+// out together with the length, in one memory round (NB = ceil(parts / 8),
+// at most 4); slots past nparts are masked afterwards (their contents are
+// whatever the workspace held).  Rows of more than 8 * NB parts load the
+// rest eight slots at a time.
+template <int D, int NB>
 __global__ __launch_bounds__(256) void merge_split_kernel(TreeParams P) {
   constexpr int PER = D / 64;
+  constexpr int NS = 8 * NB;  // slots loaded in the first round
   const int lane = threadIdx.x & 63;
   const size_t row = (size_t)blockIdx.x * 4 + (threadIdx.x >> 6);  // (b*N+node)*Hq+h
   if (row >= (size_t)P.batch * P.nodes * P.hq) return;
@@ -1020,13 +1022,15 @@ __global__ __launch_bounds__(256) void merge_split_kernel(TreeParams P) {
     for (int j = 0; j < PER; ++j) v[j] = src[64 * j];
   };
   const float2 ml0 = *reinterpret_cast<const float2*>(P.part_ml + 2 * (base + min(lane, P.parts - 1)));
-  float v[8][PER];
+  float v[NS][PER];
 #pragma unroll
-  for (int u = 0; u < 8; ++u) load_slot(min(u, P.parts - 1), v[u]);
+  for (int u = 0; u < NS; ++u) load_slot(min(u, P.parts - 1), v[u]);
+  // Nothing that waits for the length moves above the last slot load.
+  __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int j = 0; j < PER; ++j)
 #pragma unroll
-    for (int u = 0; u < 8; ++u) asm volatile("" ::"v"(v[u][j]));
+    for (int u = 0; u < NS; ++u) asm volatile("" ::"v"(v[u][j]));
   const int len = max(0, min(lraw, P.max_pages * BC_PAGE_SIZE));
   const int ntot = (len + kTile - 1) / kTile + (P.nodes + kTile - 1) / kTile;
   const int nparts = (ntot + P.tiles_per_part - 1) / P.tiles_per_part;  // >= 1
@@ -1036,27 +1040,45 @@ __global__ __launch_bounds__(256) void merge_split_kernel(TreeParams P) {
   const float mm = wave_max(mp);
   const float w = fast_exp2(mp - mm);  // every row sees its own node: mm finite
   const float lsum = wave_sum(w * lp);
+  auto weight = [&](int i) {
+    return __builtin_bit_cast(float,
+                              __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), i));
+  };
   float a[PER];
 #pragma unroll
   for (int j = 0; j < PER; ++j) a[j] = 0.f;
-  for (int i0 = 0; i0 < nparts; i0 += 8) {
-    if (i0 > 0) {
 #pragma unroll
-      for (int u = 0; u < 8; ++u) load_slot(min(i0 + u, nparts - 1), v[u]);
+  for (int u = 0; u < NS; ++u) {
+    if (u < nparts) {  // uniform
+      const float wi = weight(u);
+#pragma unroll
+      for (int j = 0; j < PER; ++j) a[j] += wi * v[u][j];
     }
+  }
+  for (int i0 = NS; i0 < nparts; i0 += 8) {
+    float x[8][PER];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) load_slot(min(i0 + u, nparts - 1), x[u]);
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
       if (i0 + u < nparts) {  // uniform
-        const float wi = __builtin_bit_cast(
-            float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), i0 + u));
+        const float wi = weight(i0 + u);
 #pragma unroll
-        for (int j = 0; j < PER; ++j) a[j] += wi * v[u][j];
+        for (int j = 0; j < PER; ++j) a[j] += wi * x[u][j];
       }
     }
   }
   const float inv = 1.f / lsum;
 #pragma unroll
   for (int j = 0; j < PER; ++j) P.out[row * D + lane + 64 * j] = a[j] * inv;
+}
+
+template <int D>
+void launch_merge_split(const TreeParams& P, dim3 grid, hipStream_t st) {
+  if (P.parts <= 8) merge_split_kernel<D, 1><<<grid, 256, 0, st>>>(P);
+  else if (P.parts <= 16) merge_split_kernel<D, 2><<<grid, 256, 0, st>>>(P);
+  else if (P.parts <= 24) merge_split_kernel<D, 3><<<grid, 256, 0, st>>>(P);
+  else merge_split_kernel<D, 4><<<grid, 256, 0, st>>>(P);
 }
 
 // Row-sharing variant for trees of four or more row tiles per (request, KV
@@ -1524,8 +1546,8 @@ hipError_t launch_split(TreeParams& P, int dim, const SplitPlan& plan, void* wor
   if (err != hipSuccess || plan.parts < 2) return err;
   const size_t rows = (size_t)P.batch * P.nodes * P.hq;
   const dim3 mgrid((unsigned)((rows + 3) / 4));
-  if (dim == 64) merge_split_kernel<64><<<mgrid, 256, 0, st>>>(P);
-  else merge_split_kernel<128><<<mgrid, 256, 0, st>>>(P);
+  if (dim == 64) launch_merge_split<64>(P, mgrid, st);
+  else launch_merge_split<128>(P, mgrid, st);
   return hipGetLastError();
 }
 
