@@ -1,0 +1,154 @@
+"""Seeded random shapes through every compute entry point, against the CPU
+oracle.
+
+Each case draws its shape from a fixed seed: batch, per-request lengths
+(empty requests included), page sharing between requests, GQA layout
+(groups 1 to 8), head dimension 64 or 128, tree size and parent shape, split
+count and cache layout.  The host's plan choices -- single pass, four- or
+eight-wave parts, two requests per workgroup, the row-sharing tree kernel,
+unsplit and flat-range decode, one or four merge waves per row -- are then
+crossed at many boundaries instead of the handful the fixed cases pin.
+Sizes are bounded so the oracle finishes in about a second per case; the
+gate is the reference driver's 3e-4 (src/main.cu:505-509), plus half an FP16
+ulp for FP16 outputs.
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle_np
+import branchcraft_capi as capi
+import gpu_helpers as G
+
+pytestmark = pytest.mark.gpu
+
+LAYOUTS = [(32, 8), (8, 8), (16, 2), (8, 1), (64, 8), (12, 3), (4, 4), (24, 8)]
+
+
+def _parents(rng, batch, nodes, kind):
+    """Valid trees (parent[i] < i, parent[0] = -1) of three shapes."""
+    if kind == "random":
+        return oracle_np.random_parents(rng, batch, nodes)
+    row = np.arange(-1, nodes - 1, dtype=np.int32)  # chain: depth nodes - 1
+    if kind == "star":
+        row = np.where(np.arange(nodes) == 0, -1, 0).astype(np.int32)
+    return np.tile(row, (batch, 1))
+
+
+def _tree_case(seed):
+    rng = np.random.default_rng(7000 + seed)
+    d = int(rng.choice([64, 128]))
+    hq, hkv = LAYOUTS[rng.integers(len(LAYOUTS))]
+    nodes = int(rng.choice([1, 2, 5, 7, 16, 31, 32, 33, 64, 100, 200, 256]))
+    batch = int(rng.integers(1, 25))
+    maxlen = int(rng.choice([0, 40, 300, 700, 1500, 2500]))
+    # Bound the oracle's work (rows x attended tokens).
+    while batch > 1 and batch * nodes * hq * (maxlen + nodes) > 8e6:
+        batch = max(1, batch // 2)
+    while maxlen > 16 and batch * nodes * hq * (maxlen + nodes) > 8e6:
+        maxlen //= 2
+    lengths = rng.integers(0, maxlen + 1, size=batch).astype(np.int32)
+    if rng.random() < 0.5:
+        lengths[:] = maxlen  # one length for every request, as forked requests have
+    share = [-1 if i == 0 or rng.random() < 0.4 else int(rng.integers(0, i))
+             for i in range(batch)]
+    npg = [-(-int(x) // 16) for x in lengths]
+    max_pages = max(max(npg), 1) + int(rng.integers(0, 40))
+    cow = {i for i in range(batch) if share[i] >= 0 and rng.random() < 0.3}
+    pool = sum(npg) + len(cow) + 8
+    sigma = float(rng.choice([0.5, 1.0]))
+    k = (rng.standard_normal((pool, 16, hkv, d)) * sigma).astype(np.float16)
+    v = (rng.standard_normal((pool, 16, hkv, d)) * sigma).astype(np.float16)
+    fresh = iter(rng.permutation(pool).astype(np.int32))
+    pages = np.full((batch, max_pages), -1, dtype=np.int32)
+    for i in range(batch):
+        j = share[i]
+        for p in range(npg[i]):
+            pages[i, p] = pages[j, p] if j >= 0 and p < npg[j] else next(fresh)
+        if i in cow and npg[i] > 0:
+            pages[i, npg[i] - 1] = next(fresh)
+    dq = (rng.standard_normal((batch, nodes, hq, d)) * sigma).astype(np.float16)
+    dk = (rng.standard_normal((batch, nodes, hkv, d)) * sigma).astype(np.float16)
+    dv = (rng.standard_normal((batch, nodes, hkv, d)) * sigma).astype(np.float16)
+    par = _parents(rng, batch, nodes, str(rng.choice(["random", "chain", "star"])))
+    what = (f"seed={seed} B={batch} N={nodes} H={hq}/{hkv} D={d} maxlen={maxlen} "
+            f"pages={max_pages}")
+    return (k, v, pages, lengths, dq, dk, dv, par), what
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_random_trees(seed, oracle):
+    """bc_tree_verify and bc_tree_verify_ws on a random tree batch."""
+    fix, what = _tree_case(seed)
+    print(what, flush=True)
+    k, v, pages, lengths, dq, dk, dv, par = fix
+    expected = oracle.tree(k, v, pages, lengths, dq, dk, dv, par, threads=16)
+    for ws in (False, True):
+        out = G.tree(k, v, pages, lengths, dq, dk, dv, par, workspace=ws)
+        G.gate(out, expected, 3e-4, f"{what} workspace={ws}")
+
+
+def _decode_case(seed):
+    rng = np.random.default_rng(8000 + seed)
+    d = int(rng.choice([64, 128]))
+    hq, hkv = LAYOUTS[rng.integers(len(LAYOUTS))]
+    batch = int(rng.integers(1, 80))
+    maxlen = int(rng.choice([1, 17, 300, 1000, 3000, 9000]))
+    while batch > 1 and batch * hq * maxlen > 4e6:
+        batch = max(1, batch // 2)
+    lengths = rng.integers(0, maxlen + 1, size=batch).astype(np.int32)
+    lengths[rng.integers(batch)] = maxlen
+    q, k, v, pages, lengths = oracle_np.paged_fixture(rng, batch, hq, hkv, d, lengths,
+                                                      spare=int(rng.integers(1, 9)),
+                                                      sigma=float(rng.choice([0.5, 1.0])))
+    what = f"seed={seed} B={batch} H={hq}/{hkv} D={d} maxlen={maxlen}"
+    return (q, k, v, pages, lengths), rng, what
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_random_paged_decode(seed, oracle):
+    """bc_decode at the auto_splits choice and at two random split counts."""
+    (q, k, v, pages, lengths), rng, what = _decode_case(seed)
+    print(what, flush=True)
+    expected = oracle.decode(q, k, v, pages, lengths, threads=16)
+    b, hq, d = q.shape
+    auto = G.lib().bc_auto_splits(capi.Shape(b, hq, k.shape[2], d, pages.shape[1], k.shape[0]),
+                                  int(lengths.max()), 256)
+    for splits in sorted({int(auto), *(int(x) for x in rng.choice(
+            [1, 2, 3, 4, 7, 8, 16, 33, 64, 128], size=2, replace=False))}):
+        out = G.decode(q, k, v, pages, lengths, splits)
+        G.gate(out, expected, 3e-4, f"{what} splits={splits}")
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_random_packed_decode(seed, oracle):
+    """bc_packed_decode and bc_packed_decode_ws over a random cache layout:
+    HND, NHD or [P, 2, 16, Hkv, D]."""
+    (q, k, v, pages, lengths), rng, what = _decode_case(100 + seed)
+    P, _, hkv, d = k.shape
+    layout = str(rng.choice(["HND", "NHD", "5D"]))
+    what += f" layout={layout}"
+    print(what, flush=True)
+    kv = np.concatenate([k, v], axis=-1)  # [P, 16, Hkv, 2D]: K then V per slot
+    if layout == "HND":
+        cache = torch.from_numpy(np.ascontiguousarray(kv.transpose(0, 2, 1, 3))).cuda()
+        strides = (cache.stride(0), cache.stride(1), cache.stride(2), d)
+    elif layout == "NHD":
+        cache = torch.from_numpy(np.ascontiguousarray(kv)).cuda()
+        strides = (cache.stride(0), cache.stride(2), cache.stride(1), d)
+    else:
+        five = np.stack([k, v], axis=1)  # [P, 2, 16, Hkv, D]
+        cache = torch.from_numpy(np.ascontiguousarray(five)).cuda()
+        strides = (cache.stride(0), cache.stride(3), cache.stride(2), cache.stride(1))
+    scale = 1 / math.sqrt(d)
+    expected, _ = oracle.packed_decode(q, cache.cpu().numpy(), pages, lengths, strides, hkv,
+                                       scale, threads=16)
+    for ws in (False, True):
+        out = G.packed(q, cache, strides, hkv, P, pages, lengths, scale, workspace=ws)
+        err = np.abs(out.astype(np.float32) - expected)
+        assert np.all(np.isfinite(out)), f"{what} workspace={ws}: non-finite output"
+        assert np.all(err <= G.f16_tolerance(expected, 3e-4)), \
+            f"{what} workspace={ws}: max err {err.max():.3e}"
