@@ -589,8 +589,9 @@ __device__ __forceinline__ void wave_lds_sync() {
 // reads, V rows at a pitch for transpose reads -- and issues the next tile's
 // loads as soon as the rows are staged, so they are in flight during the
 // current tile's MFMAs.  Masks, softmax and the hi/lo P.V product are
-// tree_kernel's.  The waves merge through LDS; with one part per unit (no
-// workspace) wave 0 writes the output, otherwise every part with tiles
+// tree_kernel's.  The waves merge through LDS, each thread combining the
+// waves' states for its share of a row; with one part per unit (no
+// workspace) that share goes to the output, otherwise every part with tiles
 // writes an FP32 partial per row, slot (row, part), and merge_split_kernel
 // combines them.
 template <int D, int W, int RQ>
