@@ -921,17 +921,18 @@ __global__ __launch_bounds__(64 * W, 2) void tree_split_kernel(TreeParams P) {
   l += shfl_xor_f(l, 32);  // both lane halves share m
 
   // ---- merge each request's LN waves through LDS in one step ----
-  // Every wave stores its state; after one barrier each thread combines the
-  // LN states of its request's share of the tile (row mrow, DPT dims) and
-  // writes it.
-  constexpr int XP = D + 4;  // padded rows: a float4 access spreads over banks
-  static_assert(W * STAGE * 2 >= W * 32 * (XP + 2) * 4, "merge buffers fit");
-  float* xacc = reinterpret_cast<float*>(s_stage);  // [W][32 rows][XP]
-  // (max, sum) per wave and row, after the accumulators
-  auto s_ml = reinterpret_cast<float(*)[32][2]>(xacc + (size_t)W * 32 * XP);
-  __syncthreads();  // the staging areas are reused below
+  // Every wave stores its state in its own staging area as soon as its
+  // tiles are done: no other wave uses that area, so the stores need no
+  // barrier and overlap the waves still computing.  After one barrier each
+  // thread combines the LN states of its request's share of the tile (row
+  // mrow, DPT dims) and writes it.
+  constexpr int XP = D + 4;      // padded rows: a float4 access spreads over banks
+  constexpr int XW = STAGE / 2;  // floats in a wave's staging area
+  static_assert(32 * XP + 64 <= XW, "a wave's state fits its staging area");
+  // Wave w's state: [32 rows][XP] accumulators, then (max, sum) per row.
+  auto xw = [&](int w) { return reinterpret_cast<float*>(s_stage) + (size_t)w * XW; };
   {
-    float* dst = xacc + (size_t)wave * 32 * XP + (size_t)lr * XP;
+    float* dst = xw(wave) + (size_t)lr * XP;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
@@ -939,10 +940,7 @@ __global__ __launch_bounds__(64 * W, 2) void tree_split_kernel(TreeParams P) {
         *reinterpret_cast<float4*>(dst + 32 * dt + 8 * jq + 4 * g) =
             make_float4(acc[dt][4 * jq], acc[dt][4 * jq + 1], acc[dt][4 * jq + 2],
                         acc[dt][4 * jq + 3]);
-    if (g == 0) {
-      s_ml[wave][lr][0] = m;
-      s_ml[wave][lr][1] = l;
-    }
+    if (g == 0) *reinterpret_cast<float2*>(xw(wave) + 32 * XP + 2 * lr) = make_float2(m, l);
   }
   __syncthreads();
   constexpr int TPR = 2 * LN;   // threads per row
@@ -957,7 +955,7 @@ __global__ __launch_bounds__(64 * W, 2) void tree_split_kernel(TreeParams P) {
   float mw[LN], mm = kNegInf;
 #pragma unroll
   for (int w = 0; w < LN; ++w) {
-    mw[w] = s_ml[w0 + w][mrow][0];
+    mw[w] = xw(w0 + w)[32 * XP + 2 * mrow];
     mm = __builtin_fmaxf(mm, mw[w]);
   }
   const float ms = safe_max(mm);  // all waves empty: every weight is 0
@@ -967,8 +965,8 @@ __global__ __launch_bounds__(64 * W, 2) void tree_split_kernel(TreeParams P) {
 #pragma unroll
   for (int w = 0; w < LN; ++w) {
     const float wt = fast_exp2(mw[w] - ms);  // 0 for a wave without tiles
-    ll += wt * s_ml[w0 + w][mrow][1];
-    const float* src = xacc + ((size_t)(w0 + w) * 32 + mrow) * XP + md0;
+    ll += wt * xw(w0 + w)[32 * XP + 2 * mrow + 1];
+    const float* src = xw(w0 + w) + (size_t)mrow * XP + md0;
 #pragma unroll
     for (int j = 0; j < DPT; j += 4) {
       const float4 v4 = *reinterpret_cast<const float4*>(src + j);
