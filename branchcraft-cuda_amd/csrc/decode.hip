@@ -198,14 +198,14 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == kMaxWaves ? 3 : 2) void paged_
   constexpr int LPR = D / 8;   // lanes per token row in a page load
   constexpr int RPI = 64 / LPR;  // token rows per load instruction
   static_assert(RPI * KS == BC_PAGE_SIZE, "one page = KS loads per lane");
-  // Per-wave K/V staging; reused after the page loop by the sliced mode's
-  // merge of [wave][head][D + 4] FP32 states.
+  // Per-wave K/V staging, one contiguous area per wave (V rows, then K
+  // rows); after the page loop the sliced mode's merge puts each wave's
+  // [head][D + 4] FP32 state, then its (max, sum) per head, in that wave's
+  // own area.
   constexpr int XP = D + 4;
-  constexpr size_t kStage = (size_t)WAVES * 16 * (VP + KP) * 2;
-  constexpr size_t kMerge = (size_t)WAVES * 16 * (XP + 2) * 4;
-  __shared__ __attribute__((aligned(16))) char s_mem[kStage > kMerge ? kStage : kMerge];
-  _Float16* const s_v = reinterpret_cast<_Float16*>(s_mem);
-  _Float16* const s_k = s_v + WAVES * 16 * VP;
+  constexpr int kWaveStage = 16 * (VP + KP) * 2;  // bytes per wave
+  static_assert(16 * (XP + 2) * 4 <= kWaveStage, "a wave's merge state fits its area");
+  __shared__ __attribute__((aligned(16))) char s_mem[(size_t)WAVES * kWaveStage];
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -283,8 +283,8 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == kMaxWaves ? 3 : 2) void paged_
     }
   };
 
-  _Float16* vs = s_v + wave * 16 * VP;
-  _Float16* ks = s_k + wave * 16 * KP;
+  _Float16* vs = reinterpret_cast<_Float16*>(s_mem + (size_t)wave * kWaveStage);
+  _Float16* ks = vs + 16 * VP;
   // Transpose-read address: lane (g4, c16) names [token 4*g4 + c16/4][4*(c16%4)].
   const _Float16* vtr = vs + (4 * g4 + (c16 >> 2)) * VP + 4 * (c16 & 3);
   // Page loads read whole token rows: load s of a lane covers token
@@ -457,19 +457,19 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == kMaxWaves ? 3 : 2) void paged_
   // lane = (column CPW*w + lane/LPC, dims (lane%LPC)*DL ..).  Empty sequences
   // and empty slices carry m = -inf, l = 0 and give weight 0 (all-empty:
   // zeros, src/paged_gqa.cu:63).
+  // The state goes to the wave's own staging area, which no other wave
+  // uses: the stores need no barrier and overlap the waves still walking
+  // their pages.
   float lt = l + shfl_xor_f(l, 16);
   lt += shfl_xor_f(lt, 32);
-  __syncthreads();  // K/V staging is reused below
-  float* xs = reinterpret_cast<float*>(s_mem);           // [wave][16][XP]
-  float* xml = xs + (size_t)WAVES * 16 * XP;              // [wave][16][2]
+  auto xw = [&](int w) { return reinterpret_cast<float*>(s_mem + (size_t)w * kWaveStage); };
 #pragma unroll
   for (int t = 0; t < DT; ++t)
-    *reinterpret_cast<float4*>(xs + ((size_t)wave * 16 + c16) * XP + 16 * t + 4 * g4) =
+    *reinterpret_cast<float4*>(xw(wave) + c16 * XP + 16 * t + 4 * g4) =
         make_float4(acc[t][0], acc[t][1], acc[t][2], acc[t][3]);
-  if (g4 == 0) {
-    xml[(wave * 16 + c16) * 2] = m == kNegInf ? kNegInf : m * c;
-    xml[(wave * 16 + c16) * 2 + 1] = lt;
-  }
+  if (g4 == 0)
+    *reinterpret_cast<float2*>(xw(wave) + 16 * XP + 2 * c16) =
+        make_float2(m == kNegInf ? kNegInf : m * c, lt);
   __syncthreads();
   constexpr int CPW = 16 / WAVES;  // head columns merged per wave
   constexpr int LPC = 64 / CPW;    // lanes per column
@@ -477,15 +477,15 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == kMaxWaves ? 3 : 2) void paged_
   static_assert(DL % 2 == 0, "at least float2 merge steps");
   const int col = CPW * wave + lane / LPC, d0 = (lane % LPC) * DL;
   float mx = kNegInf;
-  for (int w = 0; w < WAVES; ++w) mx = __builtin_fmaxf(mx, xml[(w * 16 + col) * 2]);
+  for (int w = 0; w < WAVES; ++w) mx = __builtin_fmaxf(mx, xw(w)[16 * XP + 2 * col]);
   float o[DL], lsum = 0.f;
 #pragma unroll
   for (int j = 0; j < DL; ++j) o[j] = 0.f;
   for (int w = 0; w < WAVES; ++w) {
-    const float mw = xml[(w * 16 + col) * 2];
+    const float mw = xw(w)[16 * XP + 2 * col];
     const float wt = mw == kNegInf ? 0.f : fast_exp2(mw - mx);
-    lsum += wt * xml[(w * 16 + col) * 2 + 1];
-    const float* src = xs + ((size_t)w * 16 + col) * XP + d0;
+    lsum += wt * xw(w)[16 * XP + 2 * col + 1];
+    const float* src = xw(w) + col * XP + d0;
 #pragma unroll
     for (int j = 0; j < DL; j += 2) {
       const float2 v2 = *reinterpret_cast<const float2*>(src + j);
