@@ -1491,9 +1491,15 @@ SplitPlan split_plan(const bc_shape& s, int nodes, int cus) {
   // A single pass whose eight waves take two tiles or fewer each beats a
   // split, which adds the merge launch (one request over 256 tokens: 8.2
   // against 9.6 us, over 384: 8.4 against 9.3 us; 2 x 256: 8.5 against
-  // 9.6 us; 16 x 256: 10.3 against 13.2 us).  With three tiles per wave the
-  // split wins (one request over 512 tokens: 9.1 against 9.7 us).
-  if (max_tiles <= 2 * 8) return pair_requests(s.batch, u, SplitPlan{1, max_tiles, 8}, cus);
+  // 9.6 us; 16 x 256: 10.3 against 13.2 us).  Up to five tiles per wave it
+  // still wins once its units fill (tiles per wave - 1) eighths of the CUs
+  // (12 x 512 tokens: 9.5 against 12.1 us; 16 x 512: 9.4 against 12.1 us;
+  // 12 x 768: 11.2 against 13.7 us; 8 x 1024 with 16 nodes: 13.3 against
+  // 15.0 us); below that the split wins (one request over 512 tokens: 9.1
+  // against 9.7 us).
+  const int rounds = (max_tiles + 7) / 8;  // tiles per wave in a single pass
+  if (max_tiles <= 2 * 8 || (rounds <= 5 && 8 * u >= (long long)cus * (rounds - 1)))
+    return pair_requests(s.batch, u, SplitPlan{1, max_tiles, 8}, cus);
   const SplitPlan eight = plan_for(8, cus / u);
   const SplitPlan four = plan_for(4, 2LL * cus / u);
   // Waves with at least one tile, and CUs with a workgroup.

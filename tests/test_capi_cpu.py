@@ -236,8 +236,13 @@ def test_workspace_sizes():
     for batch in (1, 2, 4, 8):
         short = capi.Shape(batch, 32, 8, 128, 30, 160)  # 480 tokens + 1 draft tile
         assert lib.bc_tree_verify_workspace_size(short, 7) == 0
-        longer = capi.Shape(batch, 32, 8, 128, 31, 160)  # 496 tokens: 17 tiles
-        assert lib.bc_tree_verify_workspace_size(longer, 7) > 0
+    # Three to five tiles per wave: a single pass once the (request, KV head)
+    # units fill (tiles per wave - 1) eighths of the 256 CUs.
+    for batch, pages, split in ((4, 31, True), (8, 31, False), (8, 47, True), (12, 47, False),
+                                (12, 63, True), (16, 63, False), (16, 78, False), (16, 79, True),
+                                (16, 81, True), (8, 81, True)):
+        size = lib.bc_tree_verify_workspace_size(capi.Shape(batch, 32, 8, 128, pages, 160), 7)
+        assert (size > 0) == split, (batch, pages)
 
 
 def test_torch_ops_register_reference_schemas():

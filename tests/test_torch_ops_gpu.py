@@ -82,17 +82,17 @@ def test_tree_verify_op_on_forked_requests():
 
 def test_tree_verify_graph_replay():
     """tree_verify captured in a HIP graph: the split kernel and its merge
-    (8 requests x 700 tokens take several parts per (request, KV head)) with
+    (8 requests x 1400 tokens take several parts per (request, KV head)) with
     the output and workspace from the graph's pool, replayed with eager work
     in between; every replay equals the eager call bit for bit, which
     matches the oracle."""
     torch.manual_seed(21)
     batch, nodes, hq, hkv, dim = 8, 7, 32, 8, 128
     q = torch.randn(batch, nodes, hq, dim, device="cuda", dtype=torch.float16)
-    prefix_k = torch.randn(48, 16, hkv, dim, device="cuda", dtype=torch.float16)
+    prefix_k = torch.randn(92, 16, hkv, dim, device="cuda", dtype=torch.float16)
     prefix_v = torch.randn_like(prefix_k)
-    pages = torch.randperm(48, device="cuda").to(torch.int32)[:44].repeat(batch, 1)
-    lengths = torch.full((batch,), 700, device="cuda", dtype=torch.int32)
+    pages = torch.randperm(92, device="cuda").to(torch.int32)[:88].repeat(batch, 1)
+    lengths = torch.full((batch,), 1400, device="cuda", dtype=torch.int32)
     draft_k = torch.randn(batch, nodes, hkv, dim, device="cuda", dtype=torch.float16)
     draft_v = torch.randn_like(draft_k)
     parent = torch.tensor([[-1, 0, 0, 1, 1, 2, 2]] * batch, device="cuda", dtype=torch.int32)

@@ -106,11 +106,11 @@ def test_garbage_past_prefix_is_ignored(oracle):
 
 
 def test_mid_batch_splits_the_prefix(oracle):
-    """Sixteen requests: 128 (request, KV head, row tile) units, half the
-    CUs, so the workspace call splits each unit's tiles over several
-    workgroups and merges their partials."""
+    """Sixteen requests over 1,400 tokens: 128 (request, KV head, row tile)
+    units of 45 tiles, so the workspace call splits each unit's tiles over
+    several workgroups and merges their partials."""
     rng = np.random.default_rng(16)
-    fix = oracle_np.tree_fixture(rng, 16, 700, 7, parents="random")
+    fix = oracle_np.tree_fixture(rng, 16, 1400, 7, parents="random")
     k, v, pages, lengths, dq, dk, dv, par = fix
     b, n, hq, d = dq.shape
     shape = capi.Shape(b, hq, k.shape[2], d, pages.shape[1], k.shape[0])
@@ -165,19 +165,19 @@ def _group_fixture(rng, lengths, share, nodes=7, hq=32, hkv=8, d=128, cow_last=(
     # share request 4's, request 5 with a copied last page; 8 and 9 share
     # request 0's, 10 has its own (a last group of three)
     dict(lengths=[613, 613, 613, 400, 613, 613, 613, 613, 613, 613, 250],
-         share=[-1, 0, 0, 0, -1, 4, 4, 4, 0, 0, -1], cow_last=(5,)),
+         share=[-1, 0, 0, 0, -1, 4, 4, 4, 0, 0, -1], cow_last=(5,), extra_pages=42),
     # nine requests on one page table (a last group of one); the spare
     # page-table capacity of this and other short cases keeps them above
-    # sixteen tiles, where the workspace call splits
-    dict(lengths=[300] * 9, share=[-1] + [0] * 8, extra_pages=12),
+    # forty tiles, where the workspace call splits
+    dict(lengths=[300] * 9, share=[-1] + [0] * 8, extra_pages=62),
     # empty requests beside sharing ones (their drafts give the output)
-    dict(lengths=[300, 0, 300, 300, 300, 300, 0, 300], share=[-1] + [0] * 7, extra_pages=12),
+    dict(lengths=[300, 0, 300, 300, 300, 300, 0, 300], share=[-1] + [0] * 7, extra_pages=62),
     # page tables far longer than every request (empty prefix chunks)
-    dict(lengths=[100] * 8, share=[-1] + [0] * 7, extra_pages=38),
+    dict(lengths=[100] * 8, share=[-1] + [0] * 7, extra_pages=74),
     # D = 64, group 4, eight nodes (32 rows)
     dict(lengths=[517] * 8, share=[-1] + [0] * 7, nodes=8, hq=8, hkv=2, d=64),
     # group 1: 32 nodes fill the row tile and the draft tile
-    dict(lengths=[290] * 8, share=[-1] + [0] * 7, nodes=32, hq=8, hkv=8, extra_pages=12),
+    dict(lengths=[290] * 8, share=[-1] + [0] * 7, nodes=32, hq=8, hkv=8, extra_pages=62),
     # five requests, two page tables
     dict(lengths=[613, 613, 400, 613, 613], share=[-1, 0, 0, -1, 3]),
 ])
