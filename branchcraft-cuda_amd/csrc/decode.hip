@@ -7,16 +7,17 @@
 // (src/packed_decode.cu:15-60).  The reference runs one 32-lane warp per
 // query head and walks tokens serially with a shuffle reduction per token.
 //
-// A workgroup holds one wave64 per KV head (up to four) and walks a flat
-// range of pages, so the waves together stream every page as whole 16-slot
-// blocks.  The range is either one whole sequence or, for split decode, an
-// equal share of all the batch's pages: workgroup w of W takes pages
-// [w*T/W, (w+1)*T/W) of the concatenated sequences, crossing sequence
-// boundaries as it goes, so every workgroup does the same work however
-// ragged the lengths are.  A sequence that ends inside one workgroup's
-// range is written directly; the others leave an FP32 partial (max, sum,
-// acc) per workgroup and a merge kernel combines them.  Inside a wave, one 16-token page and the
-// query heads of one KV head (the GQA group, up to 16) form MFMA tiles:
+// Two modes.  Split decode (flat ranges): a workgroup holds one wave64 per
+// head block (up to four) and walks an equal share of all the batch's
+// pages: workgroup w of W takes pages [w*T/W, (w+1)*T/W) of the
+// concatenated sequences, crossing sequence boundaries as it goes, so every
+// workgroup does the same work however ragged the lengths are.  A sequence
+// that ends inside one workgroup's range is written directly; the others
+// leave an FP32 partial (max, sum, acc) per workgroup and a merge kernel
+// combines them.  Unsplit decode: one workgroup per (sequence, head block)
+// whose eight waves take eighths of the sequence's pages and merge their
+// states through LDS.  Inside a wave, one 16-token page and the query heads
+// of one KV head (the GQA group, up to 16) form MFMA tiles:
 //
 //   S^T[16 tok x 16 heads] = K[16 tok x D] . Q^T[D x 16 heads]
 //       (D/32 x v_mfma_f32_16x16x32_f16; A operand lane = (token, 8-dim slice))
@@ -33,9 +34,9 @@
 // V^T through ds_read_b64_tr_b16.  The per-head softmax
 // statistics (running max over raw scores, sum) use two cross-row lane
 // shuffles per page; scale*log2e is folded into the exp2 argument and the
-// output rescale is skipped unless a running max grows.  Page ids are scalar
-// loads fetched an iteration early, and each page's K/V loads are issued while
-// the previous page is being processed.
+// output rescale is skipped unless a running max grows.  Each page's K/V
+// loads are issued while the previous page is being processed, and page ids
+// are read ahead of their pages (two pages ahead with flat ranges).
 #include "bc_device.h"
 #include "bc_host.h"
 
