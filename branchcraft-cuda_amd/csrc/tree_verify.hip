@@ -24,7 +24,9 @@
 //    a range of 32-token tiles (draft tiles first, then prefix tiles), its
 //    waves take the range's tiles round-robin with whole-row 16-byte loads
 //    staged through per-wave LDS, and merge through LDS; with parts > 1
-//    merge_split_kernel combines the FP32 partials.  Workgroup ids put
+//    merge_split_kernel combines the FP32 partials.  A single pass over
+//    more units than CUs may give one eight-wave workgroup two requests,
+//    four waves each on the same tiles.  Workgroup ids put
 //    (KV head, row tile) in the low bits, so requests that share prefix
 //    pages run on the same XCD and reuse its L2.
 //  - tree_rows_kernel: trees of many row tiles per (request, KV head), whose
