@@ -11,9 +11,13 @@ crossed at many boundaries instead of the handful the fixed cases pin.
 Sizes are bounded so the oracle finishes in about a second per case; the
 gate is the reference driver's 3e-4 (src/main.cu:505-509), plus half an FP16
 ulp for FP16 outputs.
+
+BC_RANDOM_SEEDS=n runs seeds 1000 .. 1000 + n - 1 in each test instead of
+the short default set, for a longer sweep.
 """
 
 import math
+import os
 
 import numpy as np
 import pytest
@@ -24,6 +28,13 @@ import branchcraft_capi as capi
 import gpu_helpers as G
 
 pytestmark = pytest.mark.gpu
+
+_WIDE = int(os.environ.get("BC_RANDOM_SEEDS", "0"))
+
+
+def _seeds(n):
+    return range(1000, 1000 + _WIDE) if _WIDE > 0 else range(n)
+
 
 LAYOUTS = [(32, 8), (8, 8), (16, 2), (8, 1), (64, 8), (12, 3), (4, 4), (24, 8)]
 
@@ -79,7 +90,7 @@ def _tree_case(seed):
     return (k, v, pages, lengths, dq, dk, dv, par), what
 
 
-@pytest.mark.parametrize("seed", range(24))
+@pytest.mark.parametrize("seed", _seeds(24))
 def test_random_trees(seed, oracle):
     """bc_tree_verify and bc_tree_verify_ws on a random tree batch."""
     fix, what = _tree_case(seed)
@@ -108,7 +119,7 @@ def _decode_case(seed):
     return (q, k, v, pages, lengths), rng, what
 
 
-@pytest.mark.parametrize("seed", range(16))
+@pytest.mark.parametrize("seed", _seeds(16))
 def test_random_paged_decode(seed, oracle):
     """bc_decode at the auto_splits choice and at two random split counts."""
     (q, k, v, pages, lengths), rng, what = _decode_case(seed)
@@ -123,7 +134,7 @@ def test_random_paged_decode(seed, oracle):
         G.gate(out, expected, 3e-4, f"{what} splits={splits}")
 
 
-@pytest.mark.parametrize("seed", range(16))
+@pytest.mark.parametrize("seed", _seeds(16))
 def test_random_packed_decode(seed, oracle):
     """bc_packed_decode and bc_packed_decode_ws over a random cache layout:
     HND, NHD or [P, 2, 16, Hkv, D]."""
