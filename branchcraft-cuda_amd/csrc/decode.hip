@@ -160,14 +160,22 @@ __device__ int seq_by_rank(const AttnParams& P, int lane, int rank, int& len) {
   return b;
 }
 
-template <typename OutT>
+// Four consecutive outputs: one vector store when the launch checked the
+// buffer's 16-byte alignment (VEC), else four element stores.
+template <typename OutT, bool VEC>
 __device__ __forceinline__ void store4(void* out, size_t idx, float a, float b,
                                        float c, float d) {
-  if constexpr (sizeof(OutT) == 4) {
-    *reinterpret_cast<float4*>(static_cast<float*>(out) + idx) = make_float4(a, b, c, d);
+  OutT* p = static_cast<OutT*>(out) + idx;
+  if constexpr (!VEC) {
+    p[0] = (OutT)a;
+    p[1] = (OutT)b;
+    p[2] = (OutT)c;
+    p[3] = (OutT)d;
+  } else if constexpr (sizeof(OutT) == 4) {
+    *reinterpret_cast<float4*>(p) = make_float4(a, b, c, d);
   } else {
     const f16x4 h = {(_Float16)a, (_Float16)b, (_Float16)c, (_Float16)d};
-    *reinterpret_cast<f16x4*>(static_cast<_Float16*>(out) + idx) = h;
+    *reinterpret_cast<f16x4*>(p) = h;
   }
 }
 
@@ -268,15 +276,14 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == kMaxWaves ? 3 : 2) void paged_
       const size_t o = ((size_t)pb * P.hq + h) * D + 4 * g4;
 #pragma unroll
       for (int t = 0; t < DT; ++t)
-        store4<OutT>(P.out, o + 16 * t, acc[t][0] * inv, acc[t][1] * inv,
-                     acc[t][2] * inv, acc[t][3] * inv);
+        store4<OutT, VEC>(P.out, o + 16 * t, acc[t][0] * inv, acc[t][1] * inv,
+                          acc[t][2] * inv, acc[t][3] * inv);
     } else {
       const size_t r = (size_t)(rid + pb) * P.hq + h;
       float* pa = P.part_acc + r * D + 4 * g4;
 #pragma unroll
       for (int t = 0; t < DT; ++t)
-        *reinterpret_cast<float4*>(pa + 16 * t) =
-            make_float4(acc[t][0], acc[t][1], acc[t][2], acc[t][3]);
+        store4<float, VEC>(pa, 16 * t, acc[t][0], acc[t][1], acc[t][2], acc[t][3]);
       if (g4 == 0) {
         P.part_ml[2 * r] = m == kNegInf ? kNegInf : m * c;
         P.part_ml[2 * r + 1] = lt;
@@ -674,8 +681,12 @@ hipError_t launch(AttnParams& P, int dim, hipStream_t st) {
   // Flat mode: one wave per head block, up to four per workgroup.  Sliced
   // mode: kSlices waves on one head block, each on a share of the pages.
   P.waves = P.nwg == 0 ? kSlices : P.zdim >= kMaxWaves ? kMaxWaves : P.zdim;
+  // 16-byte loads and stores need every buffer they touch aligned: a
+  // caller's output or split scratch that is only element-aligned takes the
+  // element-wise path too.
   const bool vec = aligned16(P.q) && aligned16(P.kbase) &&
-                   aligned16(P.vbase) &&
+                   aligned16(P.vbase) && aligned16(P.out) &&
+                   (P.nwg == 0 || aligned16(P.part_acc)) &&
                    (P.page_stride | P.head_stride | P.slot_stride) % 8 == 0;
   return dim == 64 ? launch_dim<64, OutT>(P, vec, st)
                    : launch_dim<128, OutT>(P, vec, st);

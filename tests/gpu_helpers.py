@@ -28,18 +28,47 @@ def dev(a, dtype=None) -> torch.Tensor:
     return t.to("cuda")
 
 
+def dev_at(a, shift: int) -> torch.Tensor:
+    """Device copy of `a` starting `shift` bytes past a 16-byte boundary (the
+    caching allocator's blocks are 512-byte aligned); shift 0 is dev(a)."""
+    t = torch.from_numpy(np.ascontiguousarray(a))
+    if shift == 0:
+        return t.to("cuda")
+    es = t.element_size()
+    assert shift % es == 0 and 0 < shift < 16
+    buf = torch.empty(t.numel() + 16 // es, device="cuda", dtype=t.dtype)
+    view = buf[shift // es:][:t.numel()]
+    view.copy_(t.reshape(-1))
+    assert view.data_ptr() % 16 == shift
+    return view.view(t.shape)
+
+
+def nan_out(shape, shift: int, dtype=torch.float32) -> torch.Tensor:
+    """Output buffer filled with NaN, `shift` bytes off 16-byte alignment."""
+    n = math.prod(shape)
+    buf = torch.full((n + 8,), float("nan"), device="cuda", dtype=dtype)
+    es = buf.element_size()
+    assert shift % es == 0 and 0 <= shift < 16
+    view = buf[shift // es:][:n]
+    assert view.data_ptr() % 16 == shift
+    return view.view(shape)
+
+
 def check(err: int, what: str) -> None:
     assert err == capi.BC_SUCCESS, f"{what} returned {err}"
 
 
-def decode(q, k, v, pages, lengths, splits, *, keep=False, out=None):
-    """bc_decode on numpy inputs; returns the FP32 output as numpy."""
+def decode(q, k, v, pages, lengths, splits, *, shift=0, out_shift=None, scratch_shift=0):
+    """bc_decode on numpy inputs; returns the FP32 output as numpy.  shift
+    places Q, K and V that many bytes off 16-byte alignment (the element-wise
+    path), out_shift the output (default: 4 bytes when shift is set) and
+    scratch_shift the split partials."""
     b, hq, d = q.shape
     P, _, hkv, _ = k.shape
-    tq, tk, tv = dev(q), dev(k), dev(v)
+    tq, tk, tv = dev_at(q, shift), dev_at(k, shift), dev_at(v, shift)
     tp, tl = dev(pages.astype(np.int32)), dev(lengths.astype(np.int32))
-    o = torch.full((b, hq, d), float("nan"), device="cuda", dtype=torch.float32)
-    pa = torch.empty(max(1, splits * b * hq * d), device="cuda", dtype=torch.float32)
+    o = nan_out((b, hq, d), 4 * (shift > 0) if out_shift is None else out_shift)
+    pa = nan_out((max(1, splits * b * hq * d),), scratch_shift)
     pml = torch.empty(max(1, splits * b * hq * 2), device="cuda", dtype=torch.float32)
     shape = capi.Shape(b, hq, hkv, d, pages.shape[1], P)
     ins = capi.Inputs(tq.data_ptr(), tk.data_ptr(), tv.data_ptr(), tp.data_ptr(),
@@ -50,17 +79,18 @@ def decode(q, k, v, pages, lengths, splits, *, keep=False, out=None):
     return o.cpu().numpy()
 
 
-def tree(k, v, pages, lengths, dq, dk, dv, parent, *, workspace=True, ws_offset=0):
+def tree(k, v, pages, lengths, dq, dk, dv, parent, *, workspace=True, ws_offset=0, shift=0):
     """bc_tree_verify_ws (workspace) or bc_tree_verify.  ws_offset shifts the
     workspace pointer by that many bytes (the size passed stays the required
-    one)."""
+    one); shift places the FP16 tensors and the output that many bytes off
+    16-byte alignment (the element-wise path)."""
     b, n, hq, d = dq.shape
     P, _, hkv, _ = k.shape
-    tk, tv = dev(k), dev(v)
+    tk, tv = dev_at(k, shift), dev_at(v, shift)
     tp, tl = dev(pages.astype(np.int32)), dev(lengths.astype(np.int32))
-    tq, tdk, tdv = dev(dq), dev(dk), dev(dv)
+    tq, tdk, tdv = dev_at(dq, shift), dev_at(dk, shift), dev_at(dv, shift)
     tpar = dev(parent.astype(np.int32))
-    o = torch.full((b, n, hq, d), float("nan"), device="cuda", dtype=torch.float32)
+    o = nan_out((b, n, hq, d), 4 * (shift > 0))
     shape = capi.Shape(b, hq, hkv, d, pages.shape[1], P)
     prefix = capi.Inputs(None, tk.data_ptr(), tv.data_ptr(), tp.data_ptr(), tl.data_ptr(),
                          None)
@@ -79,14 +109,14 @@ def tree(k, v, pages, lengths, dq, dk, dv, parent, *, workspace=True, ws_offset=
 
 
 def packed(q, cache: torch.Tensor, strides, hkv, phys_pages, pages, lengths, scale, *,
-           workspace=True, ws_offset=0):
+           workspace=True, ws_offset=0, out_shift=0):
     """cache: a GPU FP16 tensor whose storage holds the packed pool; strides
     are element strides relative to cache.data_ptr().  ws_offset shifts the
-    workspace pointer by that many bytes."""
+    workspace pointer by that many bytes, out_shift the FP16 output."""
     b, hq, d = q.shape
     tq = dev(q)
     tp, tl = dev(pages.astype(np.int32)), dev(lengths.astype(np.int32))
-    o = torch.full((b, hq, d), float("nan"), device="cuda", dtype=torch.float16)
+    o = nan_out((b, hq, d), out_shift, torch.float16)
     shape = capi.Shape(b, hq, hkv, d, pages.shape[1], phys_pages)
     bs, hs, ss, kvs = (int(x) for x in strides)
     L = lib()

@@ -92,14 +92,16 @@ def _tree_case(seed):
 
 @pytest.mark.parametrize("seed", _seeds(24))
 def test_random_trees(seed, oracle):
-    """bc_tree_verify and bc_tree_verify_ws on a random tree batch."""
+    """bc_tree_verify and bc_tree_verify_ws on a random tree batch, and one
+    of them again with every FP16 tensor off 16-byte alignment."""
     fix, what = _tree_case(seed)
     print(what, flush=True)
     k, v, pages, lengths, dq, dk, dv, par = fix
     expected = oracle.tree(k, v, pages, lengths, dq, dk, dv, par, threads=16)
-    for ws in (False, True):
-        out = G.tree(k, v, pages, lengths, dq, dk, dv, par, workspace=ws)
-        G.gate(out, expected, 3e-4, f"{what} workspace={ws}")
+    shift = 2 + 4 * (seed % 3)  # 2, 6 or 10 bytes
+    for ws, sh in ((False, 0), (True, 0), (seed % 2 == 0, shift)):
+        out = G.tree(k, v, pages, lengths, dq, dk, dv, par, workspace=ws, shift=sh)
+        G.gate(out, expected, 3e-4, f"{what} workspace={ws} shift={sh}")
 
 
 def _decode_case(seed):
@@ -121,7 +123,9 @@ def _decode_case(seed):
 
 @pytest.mark.parametrize("seed", _seeds(16))
 def test_random_paged_decode(seed, oracle):
-    """bc_decode at the auto_splits choice and at two random split counts."""
+    """bc_decode at the auto_splits choice and at two random split counts,
+    then at the auto choice with Q, K, V and the output off 16-byte
+    alignment."""
     (q, k, v, pages, lengths), rng, what = _decode_case(seed)
     print(what, flush=True)
     expected = oracle.decode(q, k, v, pages, lengths, threads=16)
@@ -132,12 +136,16 @@ def test_random_paged_decode(seed, oracle):
             [1, 2, 3, 4, 7, 8, 16, 33, 64, 128], size=2, replace=False))}):
         out = G.decode(q, k, v, pages, lengths, splits)
         G.gate(out, expected, 3e-4, f"{what} splits={splits}")
+    shift = 2 + 4 * (seed % 3)
+    out = G.decode(q, k, v, pages, lengths, int(auto), shift=shift)
+    G.gate(out, expected, 3e-4, f"{what} splits={int(auto)} shift={shift}")
 
 
 @pytest.mark.parametrize("seed", _seeds(16))
 def test_random_packed_decode(seed, oracle):
     """bc_packed_decode and bc_packed_decode_ws over a random cache layout:
-    HND, NHD or [P, 2, 16, Hkv, D]."""
+    HND, NHD or [P, 2, 16, Hkv, D]; then one of them with the FP16 output
+    off 16-byte alignment."""
     (q, k, v, pages, lengths), rng, what = _decode_case(100 + seed)
     P, _, hkv, d = k.shape
     layout = str(rng.choice(["HND", "NHD", "5D"]))
@@ -157,9 +165,11 @@ def test_random_packed_decode(seed, oracle):
     scale = 1 / math.sqrt(d)
     expected, _ = oracle.packed_decode(q, cache.cpu().numpy(), pages, lengths, strides, hkv,
                                        scale, threads=16)
-    for ws in (False, True):
-        out = G.packed(q, cache, strides, hkv, P, pages, lengths, scale, workspace=ws)
+    shift = 2 + 4 * (seed % 3)
+    for ws, sh in ((False, 0), (True, 0), (seed % 2 == 0, shift)):
+        out = G.packed(q, cache, strides, hkv, P, pages, lengths, scale, workspace=ws,
+                       out_shift=sh)
         err = np.abs(out.astype(np.float32) - expected)
-        assert np.all(np.isfinite(out)), f"{what} workspace={ws}: non-finite output"
+        assert np.all(np.isfinite(out)), f"{what} workspace={ws} shift={sh}: non-finite output"
         assert np.all(err <= G.f16_tolerance(expected, 3e-4)), \
-            f"{what} workspace={ws}: max err {err.max():.3e}"
+            f"{what} workspace={ws} shift={sh}: max err {err.max():.3e}"
