@@ -667,7 +667,7 @@ def main():
             "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": C5_HBM_TRAFFIC_BYTES,
             "traffic_source": "rocprofv3 FETCH_SIZE (x2) + WRITE_SIZE (x1) per call, scaled "
                               "by a 512 MiB copy; profiles/packed_decode_c5_hbm_traffic.md",
-            "kernel": ("paged_attn_kernel<128,_Float16,true> + merge_kernel<128,_Float16> "
+            "kernel": ("paged_attn_kernel<128,_Float16,true,4> + merge_kernel<128,_Float16,1> "
                        "(one bc_packed_decode_ws call; achieved = algorithmic bytes / "
                        "HIP-event time per call on the launch stream)"),
             "algorithmic_bytes_per_launch": c5.bytes,
