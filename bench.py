@@ -13,9 +13,13 @@ warm-ups, 7 trials x 20 launches, median; src/main.cu:354-373):
   C1 paged decode B=1 L=512;  C2 tree_verify 1 x 2048 + 7 nodes;
   C3 tree_verify 8 x (2048+5) shared prefix vs the expanded-prefix decode,
      plus the copy-on-write commit;  C4 split-K decode B=4, L~U[16K, 32K];
-  C5 packed decode without the workspace (single partition per sequence),
-     and 20 calls captured in one HIP graph and replayed (per-call time);
-     paged decode (bc_decode, separate K and V) on the same C5 sequences.
+  C5 packed decode through the reference's signature (bc_packed_decode,
+     whose split scratch is a slot of the library's pool), and 20 calls
+     captured in one HIP graph and replayed (per-call time); paged decode
+     (bc_decode, separate K and V) on the same C5 sequences; one 32K-token
+     packed sequence through both calls.
+  Tree results time bc_tree_verify_ws and the reference's signature
+  bc_tree_verify (whose split scratch is a pool slot).
 The CPU baseline times the C oracle (oracle/bc_oracle.c) on the whole C5
 workload on this host's cores.
 
@@ -54,7 +58,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--only", default="",
-                    help="comma list of configs to run (c1..c5; tl = a 256-node tree)")
+                    help="comma list of configs to run (c1..c5; tl = a 256-node tree; "
+                         "long = one 32K-token packed sequence)")
     ap.add_argument("--calibrate", action="store_true",
                     help="also run a plain 512 MiB device copy, the known-size reference "
                          "for scaling FETCH_SIZE / WRITE_SIZE counters")
@@ -255,23 +260,82 @@ class C5:
         self.bytes = decode_bytes(self.lengths, self.hq, self.hkv, self.d, 2)
 
     def call(self, cx, workspace=True):
-        lib, st = cx.lib, cx.stream()
-        bs, hs, ss, kvs = self.strides
-        args = (self.shape, self.q.data_ptr(), self.cache.data_ptr(), self.tp.data_ptr(),
-                self.tl.data_ptr(), self.out.data_ptr(), bs, hs, ss, kvs, self.scale)
-        if workspace:
-            ws, nb = self.ws.data_ptr(), self.ws_bytes
+        return packed_call(cx, self, "ws" if workspace else "reference")
 
-            def f():
-                err = lib.bc_packed_decode_ws(*args, ws, nb, st)
-                if err:
-                    raise RuntimeError(f"bc_packed_decode_ws error {err}")
-        else:
-            def f():
-                err = lib.bc_packed_decode(*args, st)
-                if err:
-                    raise RuntimeError(f"bc_packed_decode error {err}")
-        return f
+
+def packed_call(cx, p, mode):
+    """One packed-decode call on p's inputs: "ws" is bc_packed_decode_ws with
+    a caller workspace, "reference" the reference's signature
+    (bc_packed_decode: a split shape borrows a slot of the library's scratch
+    pool)."""
+    lib, st = cx.lib, cx.stream()
+    bs, hs, ss, kvs = p.strides
+    args = (p.shape, p.q.data_ptr(), p.cache.data_ptr(), p.tp.data_ptr(),
+            p.tl.data_ptr(), p.out.data_ptr(), bs, hs, ss, kvs, p.scale)
+    if mode == "ws":
+        ws, nb = p.ws.data_ptr(), p.ws_bytes
+
+        def f():
+            err = lib.bc_packed_decode_ws(*args, ws, nb, st)
+            if err:
+                raise RuntimeError(f"bc_packed_decode_ws error {err}")
+    else:
+        def f():
+            err = lib.bc_packed_decode(*args, st)
+            if err:
+                raise RuntimeError(f"bc_packed_decode error {err}")
+    return f
+
+
+class LongPacked:
+    """One 32K-token sequence in a [P, 2, 16, 8, 128] cache: the reference's
+    named next problem for packed decode (long sequences, CONTRIBUTING.md:20-23)."""
+
+    def __init__(self, cx, tokens=32768):
+        t = cx.torch
+        rng = np.random.default_rng(32)
+        self.hq, self.hkv, self.d = 32, 8, 128
+        npg = tokens // PAGE
+        self.nb = npg + 64
+        self.lengths = np.array([tokens], dtype=np.int32)
+        self.pages = block_table(rng, self.lengths, npg, self.nb)
+        g = t.Generator(device="cuda").manual_seed(32)
+        self.cache = t.randn((self.nb, 2, 16, self.hkv, self.d), generator=g, device="cuda",
+                             dtype=t.float16)
+        self.q = t.randn((1, self.hq, self.d), generator=g, device="cuda", dtype=t.float16)
+        self.out = t.empty_like(self.q)
+        self.tp = t.from_numpy(self.pages).cuda()
+        self.tl = t.from_numpy(self.lengths).cuda()
+        c = self.cache
+        self.strides = (c.stride(0), c.stride(3), c.stride(2), c.stride(1))
+        self.scale = 1.0 / math.sqrt(self.d)
+        self.shape = cx.capi.Shape(1, self.hq, self.hkv, self.d, npg, self.nb)
+        self.ws_bytes = cx.lib.bc_packed_decode_workspace_size(self.shape)
+        self.ws = t.empty(max(1, self.ws_bytes), device="cuda", dtype=t.uint8)
+        self.bytes = decode_bytes(self.lengths, self.hq, self.hkv, self.d, 2)
+
+
+def bench_packed_modes(cx, p, workload):
+    """Both packed-decode calls on p: per-call time, GB/s, and the reference
+    signature's time over the workspace call's."""
+    t = cx.torch
+    res = {}
+    outs = {}
+    for mode in ("ws", "reference"):
+        fn = packed_call(cx, p, mode)
+        us = median_us(t, fn)
+        res[f"{mode}_us"] = round(us, 3)
+        res[f"{mode}_gbs"] = round(p.bytes / us / 1e3, 1)
+        fn()
+        t.cuda.synchronize()
+        outs[mode] = p.out.clone()
+    if not t.equal(outs["ws"], outs["reference"]):
+        raise RuntimeError("reference-signature packed call differs from the workspace call")
+    res["ref_over_ws"] = round(res["reference_us"] / res["ws_us"], 3)
+    res["reference_pct_peak"] = round(100 * p.bytes / res["reference_us"] / 1e3 / HBM_PEAK_GBS,
+                                      1)
+    res.update(bytes=p.bytes, workload=workload)
+    return res
 
 
 def bench_c5_paged(cx, c5):
@@ -338,7 +402,9 @@ def tree_setup(cx, batch, prefix, seed, nodes=7):
 
 
 def tree_call(cx, f, workspace=True):
-    """bc_tree_verify_ws (workspace) or bc_tree_verify."""
+    """bc_tree_verify_ws (workspace) or bc_tree_verify (the reference's
+    signature: a plan that splits borrows a slot of the library's scratch
+    pool)."""
     capi = cx.capi
     shape = capi.Shape(f["batch"], f["hq"], f["hkv"], f["d"], f["pages"].shape[1], f["pool"])
     prefix = capi.Inputs(None, f["k"].data_ptr(), f["v"].data_ptr(), f["pages"].data_ptr(),
@@ -417,16 +483,17 @@ def bench_tree(cx, batch, prefix, seed, with_expanded, nodes=7):
     t = cx.torch
     f = tree_setup(cx, batch, prefix, seed, nodes)
     res = {}
-    calls = {"ws": tree_call(cx, f, True), "single": tree_call(cx, f, False)}
+    calls = {"ws": tree_call(cx, f, True), "ref": tree_call(cx, f, False)}
     outs = {}
     for name, fn in calls.items():
         res[f"tree_{name}_us"] = round(median_us(t, fn), 3)
         fn()
         t.cuda.synchronize()
         outs[name] = f["out"].clone()
-    res["tree_ws_vs_single_maxdiff"] = float((outs["ws"] - outs["single"]).abs().max())
+    res["tree_ws_vs_ref_maxdiff"] = float((outs["ws"] - outs["ref"]).abs().max())
+    res["tree_ref_over_ws"] = round(res["tree_ref_us"] / res["tree_ws_us"], 3)
     unique, flops = tree_metrics(f)
-    tree_us = min(res["tree_ws_us"], res["tree_single_us"])
+    tree_us = min(res["tree_ws_us"], res["tree_ref_us"])
     res.update(tree_us=tree_us, tree_bytes=unique, tree_gflop=round(flops / 1e9, 4),
                tree_gbs=round(unique / tree_us / 1e3, 1),
                tree_mfma_pct=round(100 * flops / tree_us / 1e6 / MFMA_F16_PEAK_TFLOPS, 3))
@@ -583,13 +650,16 @@ def main():
     call = c5.call(cx, workspace=True)
     # The other C5 measurements run first, so the timed loop below starts from
     # back-to-back calls (as in serving) rather than right after the 655 MB
-    # fixture was generated.
-    side = {
-        "single_partition_us": round(median_us(torch, c5.call(cx, workspace=False)), 3),
-        "reference_protocol_us": round(median_us(torch, call), 3),
-        "graph_replay_us": round(graph_replay_us(torch, lambda: c5.call(cx, workspace=True),
-                                                 c5.out), 3),
-    }
+    # fixture was generated; they follow a warm-up of their own.
+    for _ in range(50):
+        call()
+    torch.cuda.synchronize()
+    side = bench_packed_modes(cx, c5, "config 5 (the headline workload)")
+    side.pop("workload")
+    side.pop("bytes")
+    side["reference_protocol_us"] = side["ws_us"]
+    side["graph_replay_us"] = round(graph_replay_us(torch, lambda: c5.call(cx, workspace=True),
+                                                    c5.out), 3)
     for _ in range(args.warmup):
         call()
     torch.cuda.synchronize()
@@ -612,6 +682,12 @@ def main():
     }
     results["c5_paged_decode"] = bench_c5_paged(cx, c5)
     print(f"[bench] C5 paged {results['c5_paged_decode']}", file=sys.stderr, flush=True)
+    if want("long"):
+        lp = LongPacked(cx)
+        results["packed_1x32k"] = bench_packed_modes(
+            cx, lp, "packed decode, one sequence of 32768 tokens, 32/8 heads, D=128")
+        print(f"[bench] packed 1 x 32K {results['packed_1x32k']}", file=sys.stderr, flush=True)
+        del lp
     if want("c1"):
         results["c1_decode"] = bench_c1(cx)
         print(f"[bench] C1 {results['c1_decode']}", file=sys.stderr, flush=True)

@@ -24,7 +24,7 @@ BUILD = PKG / "_build"
 LIBDIR = PKG / "lib"
 LIB = LIBDIR / "libbranchcraft_hip.so"
 TORCH_EXT = PKG / "python" / "branchcraft_torch" / "_C.so"
-HIP_SOURCES = ["decode.hip", "tree_verify.hip", "commit.hip"]
+HIP_SOURCES = ["decode.hip", "tree_verify.hip", "commit.hip", "slots.hip"]
 ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
 
 # Packed-FP32 VALU forms (v_pk_{add,mul,fma}_f32) are switched off for every

@@ -8,7 +8,8 @@
 // Both are bit copies of FP16 rows, moved as 16-byte vectors when every
 // tensor pointer is 16-byte aligned and as single halves otherwise (the
 // reference accepts any `half*`); every index is range-checked on the device
-// and an out-of-range entry is skipped rather than written out of bounds.
+// and an out-of-range entry is skipped rather than written out of bounds
+// (page ids against physical_pages when the caller gives it).
 #include "bc_device.h"
 
 namespace {
@@ -67,6 +68,13 @@ bool aligned16(const void* p) {
   return (reinterpret_cast<uintptr_t>(p) & 15) == 0;
 }
 
+// Upper bound on page ids.  The reference checks no page id
+// (src/tree_attention.cu:73-89); a physical_pages below 1 means the pool size
+// is not given, and then only negative ids are skipped.
+int pool_bound(const bc_shape& s) {
+  return s.physical_pages >= 1 ? s.physical_pages : 0x7fffffff;
+}
+
 // Launches commit_kernel over `count` entries with 16-byte elements when all
 // four tensors allow it, single halves otherwise.
 hipError_t launch_commit(const bc_shape& s, const bc_half* draft_k, const bc_half* draft_v,
@@ -75,16 +83,16 @@ hipError_t launch_commit(const bc_shape& s, const bc_half* draft_k, const bc_hal
                          const int32_t* dest_slots, int request, int nodes, int count,
                          hipStream_t st) {
   const int row = s.kv_heads * s.dim;  // halves per K (or V) row
+  const int phys = pool_bound(s);
   if (aligned16(draft_k) && aligned16(draft_v) && aligned16(cache_k) && aligned16(cache_v))
     commit_kernel<uint4><<<dim3(count), kThreads, 0, st>>>(
         reinterpret_cast<const uint4*>(draft_k), reinterpret_cast<const uint4*>(draft_v),
         reinterpret_cast<uint4*>(cache_k), reinterpret_cast<uint4*>(cache_v), requests,
-        path_nodes, dest_pages, dest_slots, request, s.batch, nodes, s.physical_pages,
-        row / 8);
+        path_nodes, dest_pages, dest_slots, request, s.batch, nodes, phys, row / 8);
   else
     commit_kernel<uint16_t><<<dim3(count), kThreads, 0, st>>>(
         draft_k, draft_v, cache_k, cache_v, requests, path_nodes, dest_pages, dest_slots,
-        request, s.batch, nodes, s.physical_pages, row);
+        request, s.batch, nodes, phys, row);
   return hipGetLastError();
 }
 
@@ -96,12 +104,13 @@ extern "C" int bc_commit_path(bc_shape s, const bc_half* draft_k,
                               const int32_t* dest_pages,
                               const int32_t* dest_slots, int request,
                               int nodes, int accepted, bc_stream_t stream) {
+  // The reference's rules (src/tree_attention.cu:111-114), nothing more.
   if (!draft_k || !draft_v || !cache_k || !cache_v || !path_nodes ||
       !dest_pages || !dest_slots || request < 0 || request >= s.batch ||
-      nodes < 1 || accepted < 1 || accepted > nodes || s.kv_heads < 1 ||
-      s.physical_pages < 1)
+      nodes < 1 || accepted < 1 || accepted > nodes)
     return BC_ERROR_INVALID_VALUE;
   if (s.dim != 64 && s.dim != 128) return BC_ERROR_INVALID_VALUE;
+  if (s.kv_heads < 1) return BC_SUCCESS;  // rows of no heads: nothing to copy
   return launch_commit(s, draft_k, draft_v, cache_k, cache_v, nullptr, path_nodes,
                        dest_pages, dest_slots, request, nodes, accepted,
                        reinterpret_cast<hipStream_t>(stream));
@@ -116,9 +125,9 @@ extern "C" int bc_commit_paths(bc_shape s, const bc_half* draft_k,
                                bc_stream_t stream) {
   if (!draft_k || !draft_v || !cache_k || !cache_v || !requests || !path_nodes ||
       !dest_pages || !dest_slots || s.batch < 1 || nodes < 1 || count < 0 ||
-      s.kv_heads < 1 || s.physical_pages < 1 || (s.dim != 64 && s.dim != 128))
+      (s.dim != 64 && s.dim != 128))
     return BC_ERROR_INVALID_VALUE;
-  if (count == 0) return BC_SUCCESS;
+  if (count == 0 || s.kv_heads < 1) return BC_SUCCESS;
   return launch_commit(s, draft_k, draft_v, cache_k, cache_v, requests, path_nodes,
                        dest_pages, dest_slots, 0, nodes, count,
                        reinterpret_cast<hipStream_t>(stream));
@@ -129,22 +138,23 @@ extern "C" int bc_copy_pages(bc_shape s, bc_half* cache_k, bc_half* cache_v,
                              const int32_t* dst_pages, int count,
                              bc_stream_t stream) {
   if (!cache_k || !cache_v || !src_pages || !dst_pages || count < 0 ||
-      s.kv_heads < 1 || (s.dim != 64 && s.dim != 128) || s.physical_pages < 1)
+      (s.dim != 64 && s.dim != 128))
     return BC_ERROR_INVALID_VALUE;
-  if (count == 0) return BC_SUCCESS;
+  if (count == 0 || s.kv_heads < 1) return BC_SUCCESS;
   const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const int page = BC_PAGE_SIZE * s.kv_heads * s.dim;  // halves per page of K (or V)
+  const int phys = pool_bound(s);
   if (aligned16(cache_k) && aligned16(cache_v)) {
     const int page_vec = page / 8;
     const int slice_vec = 4 * kThreads;  // 16 KiB of K and of V per workgroup
     const int slices = (page_vec + slice_vec - 1) / slice_vec;
     copy_pages_kernel<uint4><<<dim3(count, slices), kThreads, 0, st>>>(
         reinterpret_cast<uint4*>(cache_k), reinterpret_cast<uint4*>(cache_v), src_pages,
-        dst_pages, s.physical_pages, page_vec, slice_vec);
+        dst_pages, phys, page_vec, slice_vec);
   } else {
     const int slice = 16 * kThreads;  // 8 KiB of K and of V per workgroup
     copy_pages_kernel<uint16_t><<<dim3(count, (page + slice - 1) / slice), kThreads, 0, st>>>(
-        cache_k, cache_v, src_pages, dst_pages, s.physical_pages, page, slice);
+        cache_k, cache_v, src_pages, dst_pages, phys, page, slice);
   }
   return hipGetLastError();
 }

@@ -39,6 +39,7 @@
 // are read ahead of their pages (two pages ahead with flat ranges).
 #include "bc_device.h"
 #include "bc_host.h"
+#include "bc_slots.h"
 
 #include <math.h>
 
@@ -808,13 +809,22 @@ extern "C" size_t bc_packed_decode_workspace_size(bc_shape s) {
   return packed_workspace(s, packed_nwg(s));
 }
 
+// The reference's packed_decode rules (src/packed_decode.cu:64-73) plus
+// kv_stride >= 1.
+static bool packed_args_ok(const bc_shape& s, const bc_half* q, const bc_half* kv,
+                           const int32_t* pages, const int32_t* lengths,
+                           const bc_half* output, long long bs, long long hs, long long ss,
+                           long long kvs, float scale) {
+  return shape_ok(s) && q && kv && pages && lengths && output && bs >= 1 && hs >= 1 &&
+         ss >= 1 && kvs >= 1 && scale > 0.f;
+}
+
 static int packed_common(bc_shape s, const bc_half* q, const bc_half* kv,
                          const int32_t* pages, const int32_t* lengths,
                          bc_half* output, long long bs, long long hs,
                          long long ss, long long kvs, float scale,
                          void* ws, size_t ws_bytes, bc_stream_t stream) {
-  if (!shape_ok(s) || !q || !kv || !pages || !lengths || !output || bs < 1 ||
-      hs < 1 || ss < 1 || kvs < 1 || !(scale > 0.f))
+  if (!packed_args_ok(s, q, kv, pages, lengths, output, bs, hs, ss, kvs, scale))
     return BC_ERROR_INVALID_VALUE;
   AttnParams P{};
   P.q = q;
@@ -851,9 +861,17 @@ extern "C" int bc_packed_decode(bc_shape s, const bc_half* q,
                                 long long block_stride, long long head_stride,
                                 long long slot_stride, long long kv_stride,
                                 float scale, bc_stream_t stream) {
+  if (!packed_args_ok(s, q, packed_kv, pages, lengths, output, block_stride, head_stride,
+                      slot_stride, kv_stride, scale))
+    return BC_ERROR_INVALID_VALUE;
+  // The reference's signature has no workspace: a shape that splits borrows
+  // a slot of the library's scratch pool for the call (none under graph
+  // capture or when the slot is too small: the single pass then runs).
+  const size_t need = bc_packed_decode_workspace_size(s);
+  const bch::ScratchLease lease(reinterpret_cast<hipStream_t>(stream), need);
   return packed_common(s, q, packed_kv, pages, lengths, output, block_stride,
-                       head_stride, slot_stride, kv_stride, scale, nullptr, 0,
-                       stream);
+                       head_stride, slot_stride, kv_stride, scale, lease.get(),
+                       lease.get() ? need : 0, stream);
 }
 
 extern "C" int bc_packed_decode_ws(bc_shape s, const bc_half* q,
@@ -865,6 +883,12 @@ extern "C" int bc_packed_decode_ws(bc_shape s, const bc_half* q,
                                    long long slot_stride, long long kv_stride,
                                    float scale, void* workspace,
                                    size_t workspace_bytes, bc_stream_t stream) {
+  // A workspace that cannot serve the split (null, too small, not 16-byte
+  // aligned) is ignored: the call is bc_packed_decode's.
+  if (!workspace || !aligned16(workspace) ||
+      (shape_ok(s) && workspace_bytes < bc_packed_decode_workspace_size(s)))
+    return bc_packed_decode(s, q, packed_kv, pages, lengths, output, block_stride,
+                            head_stride, slot_stride, kv_stride, scale, stream);
   return packed_common(s, q, packed_kv, pages, lengths, output, block_stride,
                        head_stride, slot_stride, kv_stride, scale, workspace,
                        workspace_bytes, stream);

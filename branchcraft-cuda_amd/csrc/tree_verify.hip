@@ -38,6 +38,7 @@
 
 #include "bc_device.h"
 #include "bc_host.h"
+#include "bc_slots.h"
 
 namespace {
 
@@ -201,8 +202,10 @@ __global__ __launch_bounds__(kThreads, 2) void tree_kernel(TreeParams P) {
       const size_t phys = (size_t)(tv ? (lr >> 4 ? ph[1] : ph[0]) : 0);
       const size_t off =
           tv ? (phys * BC_PAGE_SIZE + t % BC_PAGE_SIZE) * tok_stride + (size_t)kvh * D : 0;
-      kp = P.k + off;
-      vp = P.v + off;
+      // Rows that are not tokens read draft row 0 (always present): with the
+      // pool size not given, page 0 of the pool may not exist.
+      kp = tv ? P.k + off : P.dk;
+      vp = tv ? P.v + off : P.dv;
     } else {
       pok[0] = pok[1] = true;
       const int dn = (it - ntile_p) * kTile + lr;
@@ -1341,13 +1344,22 @@ __global__ __launch_bounds__(kThreads, 2) void tree_rows_kernel(TreeParams P) {
                    acc[dt][4 * jq + 3] * inv);
 }
 
+// The reference's rules (src/tree_attention.cu:94-99): physical_pages is not
+// among them, and a value below 1 means the pool size is not given.
 bool tree_args_ok(const bc_shape& s, const bc_tree_inputs& in, int nodes) {
   return s.batch >= 1 && s.query_heads >= 1 && s.kv_heads >= 1 &&
          s.query_heads % s.kv_heads == 0 && (s.dim == 64 || s.dim == 128) &&
-         s.max_pages >= 1 && s.physical_pages >= 1 && nodes >= 1 &&
-         nodes <= BC_MAX_TREE_NODES && in.prefix.k && in.prefix.v && in.prefix.pages && in.prefix.lengths &&
-         in.draft_q && in.draft_k && in.draft_v && in.parent && in.output;
+         s.max_pages >= 1 && nodes >= 1 && nodes <= BC_MAX_TREE_NODES && in.prefix.k &&
+         in.prefix.v && in.prefix.pages && in.prefix.lengths && in.draft_q && in.draft_k &&
+         in.draft_v && in.parent && in.output;
 }
+
+// With the pool size given, ids outside [0, physical_pages) are masked and
+// every padding load may read page 0.  Without it (physical_pages < 1, as an
+// empty pool gives), the page-table entries inside a length are trusted as in
+// the reference, and only tree_kernel runs: it reads pages for tokens inside
+// the length only and points every other row at the draft tensors.
+bool pool_known(const bc_shape& s) { return s.physical_pages >= 1; }
 
 bool aligned16(const void* p) {
   return (reinterpret_cast<uintptr_t>(p) & 15) == 0;
@@ -1371,8 +1383,9 @@ TreeParams make_params(const bc_shape& s, const bc_tree_inputs& in, int nodes) {
   P.group = s.query_heads / s.kv_heads;
   P.max_pages = s.max_pages;
   // physical_pages is not part of the reference tree contract
-  // (bindings/torch_ops.cpp:54 passes prefix_k.size(0)); 0 means unchecked.
-  P.phys_pages = s.physical_pages >= 1 ? s.physical_pages : 0x7fffffff;
+  // (bindings/torch_ops.cpp:54 passes prefix_k.size(0)); below 1 the ids
+  // are not range-checked (tree_kernel only, see pool_known).
+  P.phys_pages = pool_known(s) ? s.physical_pages : 0x7fffffff;
   P.rows = nodes * P.group;
   P.row_tiles = (P.rows + 31) / 32;
   P.scale_log2 = (float)(1.4426950408889634 / __builtin_sqrt((double)s.dim));
@@ -1409,14 +1422,17 @@ template <int D, bool VEC>
 void launch_tree_kernel(const TreeParams& P, bool rows_kernel, dim3 grid, hipStream_t st) {
   if (rows_kernel)
     tree_rows_kernel<D, VEC><<<grid, kThreads, 0, st>>>(P);
-  else  // only unaligned tensors get here: the split kernel takes the rest
+  else  // unaligned tensors or an unknown pool size: the split kernel takes the rest
     tree_kernel<D, false><<<grid, kThreads, 0, st>>>(P);
 }
 
 // vec: every FP16 tensor and the output are 16-byte aligned (16-byte loads
 // and stores); otherwise the kernels move single halves and floats.
-hipError_t launch_tree(const TreeParams& P, int dim, bool vec, hipStream_t st) {
-  const bool rows_kernel = rows_kernel_for(P.batch, P.hkv, P.row_tiles, bch::device_cus());
+// known_pool: false sends every shape to tree_kernel (see pool_known).
+hipError_t launch_tree(const TreeParams& P, int dim, bool vec, bool known_pool,
+                       hipStream_t st) {
+  const bool rows_kernel =
+      known_pool && rows_kernel_for(P.batch, P.hkv, P.row_tiles, bch::device_cus());
   const dim3 grid((unsigned)((size_t)P.batch * P.hkv * row_units(P.row_tiles, rows_kernel)));
   if (dim == 64) {
     if (vec) launch_tree_kernel<64, true>(P, rows_kernel, grid, st);
@@ -1567,14 +1583,26 @@ extern "C" int bc_tree_verify(bc_shape s, bc_tree_inputs in, int nodes,
   const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const bool vec = tree_ptrs_aligned(in);
   const int cus = bch::device_cus();
-  if (vec && !rows_kernel_for(P.batch, P.hkv, P.row_tiles, cus)) {
+  const bool known = pool_known(s);
+  if (vec && known && !rows_kernel_for(P.batch, P.hkv, P.row_tiles, cus)) {
+    // The reference's signature has no workspace: a plan that splits the
+    // prefix borrows a slot of the library's scratch pool for the call
+    // (none under graph capture or when the slot is too small: the single
+    // pass below then runs).
+    const SplitPlan plan = split_plan(s, nodes, cus);
+    size_t acc = 0;
+    const size_t need = split_workspace(s, nodes, plan, &acc);
+    if (need > 0) {
+      const bch::ScratchLease lease(st, need);
+      if (lease.get()) return launch_split(P, s.dim, plan, lease.get(), acc, st);
+    }
     const int max_tiles =
         (s.max_pages * BC_PAGE_SIZE + kTile - 1) / kTile + (nodes + kTile - 1) / kTile;
     const long long units = (long long)P.batch * P.hkv * P.row_tiles;
     return launch_split(P, s.dim, pair_requests(P.batch, units, SplitPlan{1, max_tiles, 8}, cus),
                         nullptr, 0, st);
   }
-  return launch_tree(P, s.dim, vec, st);
+  return launch_tree(P, s.dim, vec, known, st);
 }
 
 namespace {
@@ -1582,8 +1610,7 @@ namespace {
 bool tree_shape_ok(const bc_shape& s, int nodes) {
   return s.batch >= 1 && s.query_heads >= 1 && s.kv_heads >= 1 &&
          s.query_heads % s.kv_heads == 0 && (s.dim == 64 || s.dim == 128) &&
-         s.max_pages >= 1 && s.physical_pages >= 1 && nodes >= 1 &&
-         nodes <= BC_MAX_TREE_NODES;
+         s.max_pages >= 1 && nodes >= 1 && nodes <= BC_MAX_TREE_NODES;
 }
 
 bool split_for(const bc_shape& s, int nodes) {
@@ -1591,9 +1618,10 @@ bool split_for(const bc_shape& s, int nodes) {
   return !rows_kernel_for(s.batch, s.kv_heads, row_tiles, bch::device_cus());
 }
 
-// tree_rows_kernel and split plans of one part need no workspace.
+// tree_rows_kernel, split plans of one part and calls without the pool size
+// need no workspace.
 size_t ws_size(const bc_shape& s, int nodes) {
-  if (!split_for(s, nodes)) return 0;
+  if (!pool_known(s) || !split_for(s, nodes)) return 0;
   size_t a = 0;
   return split_workspace(s, nodes, split_plan(s, nodes, bch::device_cus()), &a);
 }
@@ -1602,8 +1630,9 @@ int tree_ws_call(bc_shape s, bc_tree_inputs in, int nodes, void* workspace,
                  size_t workspace_bytes, bc_stream_t stream) {
   if (!tree_args_ok(s, in, nodes)) return BC_ERROR_INVALID_VALUE;
   const bool vec = tree_ptrs_aligned(in);
-  // Tensors that are not 16-byte aligned take the element-wise single pass.
-  if (!vec) return bc_tree_verify(s, in, nodes, stream);
+  // Tensors that are not 16-byte aligned, and calls without the pool size,
+  // take the single pass.
+  if (!vec || !pool_known(s)) return bc_tree_verify(s, in, nodes, stream);
   if (!split_for(s, nodes)) return bc_tree_verify(s, in, nodes, stream);
   const SplitPlan plan = split_plan(s, nodes, bch::device_cus());
   size_t acc = 0;

@@ -8,7 +8,27 @@
  * fails, otherwise the launch error reported by the HIP runtime.
  *
  * FP16 tensors are passed as `const bc_half*` (IEEE binary16 bit patterns).
- * The library holds no global state and is reentrant.
+ *
+ * State, per device: a cache of the CU count, and the split-scratch pool
+ * that the entry points without a workspace argument (bc_packed_decode,
+ * bc_tree_verify) borrow from -- BC_SCRATCH_SLOTS slots of
+ * BC_SCRATCH_SLOT_BYTES in a static device array (32 MiB per GPU the
+ * library runs on, held until the process ends).  A call on a stream takes
+ * the slot that stream used last (reused in stream order), else a free
+ * slot, else the least recently used slot whose last use was recorded in
+ * the slot's event, which the stream then waits for on the device
+ * (hipStreamWaitEvent).  Events are recorded only after some call has found
+ * every slot owned by other streams; from then on after every use.  Calls
+ * on any streams and host threads may therefore overlap, and up to
+ * BC_SCRATCH_SLOTS streams run at no extra GPU cost.  Under graph capture,
+ * for shapes whose split scratch exceeds a slot, when every slot is owned
+ * by another stream with no recorded use, or when a HIP call of the pool
+ * fails, these calls run their single-pass kernels instead (same results up
+ * to floating-point reassociation).  Each slot's event is created once;
+ * nothing is allocated per call.  A stream must not be destroyed while one
+ * of its calls is still running (its handle may be reused).
+ * bc_packed_decode_noalloc uses a separate static array
+ * (BC_STATIC_SCRATCH_BYTES).
  *
  * Reference interface replaced: include/branchcraft.hpp:8-74 of
  * Haaziq386/branchcraft-cuda (namespace branchcraft, cudaError_t returns).
@@ -32,6 +52,11 @@ enum {
   BC_ERROR_INVALID_VALUE = 1, /* hipErrorInvalidValue */
   BC_ERROR_OUT_OF_MEMORY = 2, /* hipErrorOutOfMemory: a fixed scratch is too small */
 };
+
+/* The split-scratch pool of bc_packed_decode and bc_tree_verify: slots per
+ * GPU and bytes per slot. */
+#define BC_SCRATCH_SLOTS 4
+#define BC_SCRATCH_SLOT_BYTES (8u << 20)
 
 /* Tokens per KV page (reference: kPageSize, include/branchcraft.hpp:8). */
 #define BC_PAGE_SIZE 16
@@ -110,25 +135,36 @@ int bc_auto_splits(bc_shape shape, int max_length, int cu_count);
 
 /* Ancestor-only tree verification over a paged prefix.
  * Replaces branchcraft::tree_verify, include/branchcraft.hpp:55-56
- * (src/tree_attention.cu:93-105).  Runs without scratch: one workgroup
- * per (request, KV head, row tile) streams the whole prefix.  Tensors that
- * are not 16-byte aligned are read and written element by element.
- * Rejects: batch/Hq/Hkv < 1, Hq % Hkv != 0, dim not 64/128, max_pages or
- * physical_pages < 1 (page ids outside the pool read page 0, masked),
- * nodes outside [1, BC_MAX_TREE_NODES], a null K/V, page table, lengths,
- * draft tensor, parent array or output. */
+ * (src/tree_attention.cu:93-105).  Shapes whose prefix splits (as
+ * bc_tree_verify_ws would split it) run the split kernels with a slot of the
+ * library's scratch pool (see the state note at the top), giving
+ * bc_tree_verify_ws's results bit for bit; otherwise one workgroup per
+ * (request, KV head, row tile) streams the whole prefix.  Tensors that are
+ * not 16-byte aligned take an element-wise single pass.
+ * Rejects, as the reference: batch/Hq/Hkv < 1, Hq % Hkv != 0, dim not
+ * 64/128, max_pages < 1, nodes outside [1, BC_MAX_TREE_NODES], a null K/V,
+ * page table, lengths, draft tensor, parent array or output.
+ * physical_pages >= 1 gives the pool size: page ids inside a length that
+ * fall outside [0, physical_pages) are skipped.  physical_pages < 1 (an
+ * empty pool, as the torch op passes for a 0-page prefix_k) means the size
+ * is not given: ids inside a length are trusted as in the reference (only
+ * negative ones are skipped), nothing outside the lengths is read, and the
+ * call runs the single-pass kernel with every request's rows attending to
+ * the prefix tokens inside its length plus its ancestors. */
 int bc_tree_verify(bc_shape shape, bc_tree_inputs in, int nodes,
                    bc_stream_t stream);
 
 /* Bytes of workspace bc_tree_verify_ws needs for this shape (0 when the
- * shape does not benefit from splitting the prefix). */
+ * shape does not benefit from splitting the prefix, and when
+ * physical_pages < 1). */
 size_t bc_tree_verify_workspace_size(bc_shape shape, int nodes);
 
 /* bc_tree_verify with each request's tiles split over several workgroups
  * and an FP32 merge; `workspace` holds at least
- * bc_tree_verify_workspace_size bytes.  A null workspace, one smaller than required or one not aligned to
- * 16 bytes falls back to bc_tree_verify.  Results match bc_tree_verify
- * within floating-point reassociation. */
+ * bc_tree_verify_workspace_size bytes.  A null workspace, one smaller than
+ * required or one not aligned to 16 bytes is ignored and the call is
+ * bc_tree_verify's.  Results match bc_tree_verify within floating-point
+ * reassociation (bit for bit when that call splits too). */
 int bc_tree_verify_ws(bc_shape shape, bc_tree_inputs in, int nodes,
                       void* workspace, size_t workspace_bytes,
                       bc_stream_t stream);
@@ -137,10 +173,14 @@ int bc_tree_verify_ws(bc_shape shape, bc_tree_inputs in, int nodes,
  * cache[dest_pages[i], dest_slots[i]] <- draft[request, path_nodes[i]] for
  * i < accepted, K and V, bit-exact.  Entries whose node, page or slot is out
  * of range are skipped.  shape.kv_heads, shape.dim, shape.batch and
- * shape.physical_pages describe the tensors.  Any 2-byte aligned pointers
- * work (16-byte copies when all four are 16-byte aligned).
+ * shape.physical_pages describe the tensors; physical_pages < 1 means the
+ * pool size is not given (page ids are then only checked for >= 0), and
+ * kv_heads < 1 copies nothing.  Any 2-byte aligned pointers work (16-byte
+ * copies when all four are 16-byte aligned).
  * Replaces branchcraft::commit_path, include/branchcraft.hpp:61-65
- * (src/tree_attention.cu:107-122). */
+ * (src/tree_attention.cu:107-122), with its rejections: a null pointer,
+ * request outside [0, batch), nodes < 1, accepted outside [1, nodes], dim
+ * not 64/128. */
 int bc_commit_path(bc_shape shape, const bc_half* draft_k,
                    const bc_half* draft_v, bc_half* cache_k, bc_half* cache_v,
                    const int32_t* path_nodes, const int32_t* dest_pages,
@@ -151,7 +191,8 @@ int bc_commit_path(bc_shape shape, const bc_half* draft_k,
  * the K and V rows (all heads) of draft[requests[i], path_nodes[i]] into
  * cache[dest_pages[i], dest_slots[i]], for i < count.  Drafts are
  * [shape.batch, nodes, Hkv, D]; entries with a request, node, page or slot
- * out of range are skipped.  No reference counterpart: it batches the
+ * out of range are skipped (pages as for bc_commit_path; kv_heads < 1 copies
+ * nothing).  No reference counterpart: it batches the
  * per-request commit_path calls of a transaction (src/tree_attention.cu:
  * 107-122; python/branchcraft_torch/transaction.py:144-148) into one launch.
  * Entries must not write the same (page, slot) twice. */
@@ -163,7 +204,9 @@ int bc_commit_paths(bc_shape shape, const bc_half* draft_k,
 
 /* Copy whole pages (all 16 slots, K and V) cache[dst_pages[i]] <-
  * cache[src_pages[i]] for i < count: the copy-on-write clone of a shared
- * partial page.  Out-of-range page ids and src == dst are skipped.  All
+ * partial page.  Out-of-range page ids (negative, or not below
+ * physical_pages when that is >= 1) and src == dst are skipped; kv_heads < 1
+ * copies nothing.  All
  * pairs copy concurrently, so the destinations must be distinct and no
  * destination may also be a source; otherwise the result is unspecified.
  * Any 2-byte aligned pointers work.  No reference C++
@@ -181,7 +224,10 @@ int bc_copy_pages(bc_shape shape, bc_half* cache_k, bc_half* cache_v,
  * [P,Hkv,16,2D] layout; [P,2,16,Hkv,D] uses kv_stride = 16*Hkv*D.
  * Replaces branchcraft::packed_decode, include/branchcraft.hpp:70-74
  * (src/packed_decode.cu:64-82), adding kv_stride.  Rejects the bc_decode
- * shape rules plus any stride < 1 and scale <= 0 (or NaN). */
+ * shape rules plus any stride < 1 and scale <= 0 (or NaN).  Shapes that
+ * split (bc_packed_decode_workspace_size > 0) run the split kernels with a
+ * slot of the library's scratch pool (see the state note at the top), giving
+ * bc_packed_decode_ws's results bit for bit; the others run unsplit. */
 int bc_packed_decode(bc_shape shape, const bc_half* q, const bc_half* packed_kv,
                      const int32_t* pages, const int32_t* lengths,
                      bc_half* output, long long block_stride,
@@ -203,7 +249,8 @@ size_t bc_packed_decode_workspace_size(bc_shape shape);
  * size depend on the shape and the device's CU count only; the kernels find
  * the ranges from the lengths on the device, so no lengths are read on the
  * host.  A null workspace, one smaller than required or not aligned to 16
- * bytes, or a shape whose workspace size is 0, runs bc_packed_decode. */
+ * bytes is ignored and the call is bc_packed_decode's; a shape whose
+ * workspace size is 0 runs unsplit. */
 int bc_packed_decode_ws(bc_shape shape, const bc_half* q,
                         const bc_half* packed_kv, const int32_t* pages,
                         const int32_t* lengths, bc_half* output,

@@ -79,13 +79,17 @@ def decode(q, k, v, pages, lengths, splits, *, shift=0, out_shift=None, scratch_
     return o.cpu().numpy()
 
 
-def tree(k, v, pages, lengths, dq, dk, dv, parent, *, workspace=True, ws_offset=0, shift=0):
+def tree(k, v, pages, lengths, dq, dk, dv, parent, *, workspace=True, ws_offset=0, shift=0,
+         phys_pages=None):
     """bc_tree_verify_ws (workspace) or bc_tree_verify.  ws_offset shifts the
     workspace pointer by that many bytes (the size passed stays the required
     one); shift places the FP16 tensors and the output that many bytes off
-    16-byte alignment (the element-wise path)."""
+    16-byte alignment (the element-wise path); phys_pages overrides the
+    shape's pool size (default: k.shape[0])."""
     b, n, hq, d = dq.shape
     P, _, hkv, _ = k.shape
+    if phys_pages is not None:
+        P = phys_pages
     tk, tv = dev_at(k, shift), dev_at(v, shift)
     tp, tl = dev(pages.astype(np.int32)), dev(lengths.astype(np.int32))
     tq, tdk, tdv = dev_at(dq, shift), dev_at(dk, shift), dev_at(dv, shift)
@@ -137,12 +141,16 @@ def packed(q, cache: torch.Tensor, strides, hkv, phys_pages, pages, lengths, sca
 
 
 def commit(cache_k: torch.Tensor, cache_v: torch.Tensor, dk: torch.Tensor,
-           dv: torch.Tensor, path, dest_pages, dest_slots, request: int):
+           dv: torch.Tensor, path, dest_pages, dest_slots, request: int, *,
+           phys_pages=None, kv_heads=None):
+    """bc_commit_path; phys_pages and kv_heads override the shape's fields
+    (defaults: the cache's page count and the drafts' head count)."""
     b, n, hkv, d = dk.shape
     tpath = torch.tensor(path, device="cuda", dtype=torch.int32)
     tdp = torch.tensor(dest_pages, device="cuda", dtype=torch.int32)
     tds = torch.tensor(dest_slots, device="cuda", dtype=torch.int32)
-    shape = capi.Shape(b, hkv, hkv, d, 1, cache_k.shape[0])
+    kvh = hkv if kv_heads is None else kv_heads
+    shape = capi.Shape(b, kvh, kvh, d, 1, cache_k.shape[0] if phys_pages is None else phys_pages)
     check(lib().bc_commit_path(shape, dk.data_ptr(), dv.data_ptr(), cache_k.data_ptr(),
                                cache_v.data_ptr(), tpath.data_ptr(), tdp.data_ptr(),
                                tds.data_ptr(), request, n, len(path), stream()),

@@ -97,9 +97,24 @@ def test_tree_rejects_null(field):
 def test_tree_rejects_bad_shape_and_null_prefix():
     lib = capi.load()
     assert lib.bc_tree_verify(_shape(dim=80), _tree_inputs(), 7, None) == INVALID
-    ins = _tree_inputs()
-    ins.prefix.k = None
-    assert lib.bc_tree_verify(_shape(), ins, 7, None) == INVALID
+    for field in ("k", "v", "pages", "lengths"):
+        ins = _tree_inputs()
+        setattr(ins.prefix, field, None)
+        assert lib.bc_tree_verify(_shape(), ins, 7, None) == INVALID, field
+        assert lib.bc_tree_verify_ws(_shape(), ins, 7, None, 0, None) == INVALID, field
+    for bad in (dict(batch=0), dict(kv_heads=0), dict(query_heads=30), dict(max_pages=0)):
+        assert lib.bc_tree_verify(_shape(**bad), _tree_inputs(), 7, None) == INVALID, bad
+
+
+def test_tree_accepts_any_pool_size():
+    """The reference checks no pool size (src/tree_attention.cu:94-99):
+    physical_pages < 1 is not rejected; it means the size is not given, and
+    such calls need no workspace (they run the single pass)."""
+    lib = capi.load()
+    c3 = dict(batch=8, max_pages=129)
+    assert lib.bc_tree_verify_workspace_size(_shape(**c3), 7) > 0
+    for phys in (0, -1):
+        assert lib.bc_tree_verify_workspace_size(_shape(physical_pages=phys, **c3), 7) == 0
 
 
 @pytest.mark.parametrize("request_,nodes,accepted", [(-1, 7, 1), (2, 7, 1), (0, 0, 1),
@@ -111,6 +126,29 @@ def test_commit_rejects(request_, nodes, accepted):
                               accepted, None) == INVALID
     assert lib.bc_commit_path(capi.Shape(2, 8, 8, 96, 1, 16), FAKE, FAKE, FAKE, FAKE, FAKE,
                               FAKE, FAKE, 0, 7, 1, None) == INVALID
+
+
+def test_commit_checks_are_the_reference_s():
+    """bc_commit_path rejects what src/tree_attention.cu:111-114 rejects (a
+    null pointer, a request outside [0, batch), nodes < 1, accepted outside
+    [1, nodes], dim not 64/128) and nothing else: kv_heads < 1 is an empty
+    copy (success, nothing launched), and physical_pages < 1 means the pool
+    size is not given (covered on the GPU)."""
+    lib = capi.load()
+    args = [FAKE] * 7
+    for i in range(7):
+        bad = list(args)
+        bad[i] = None
+        assert lib.bc_commit_path(capi.Shape(2, 8, 8, 128, 1, 16), *bad, 0, 7, 1,
+                                  None) == INVALID
+    for kvh in (0, -3):
+        for phys in (16, 0):
+            s = capi.Shape(2, kvh, kvh, 128, 1, phys)
+            assert lib.bc_commit_path(s, *args, 1, 7, 3, None) == capi.BC_SUCCESS
+            assert lib.bc_commit_paths(s, *args[:4], FAKE, *args[4:], 7, 2,
+                                       None) == capi.BC_SUCCESS
+            assert lib.bc_copy_pages(capi.Shape(1, kvh, kvh, 64, 1, phys), FAKE, FAKE, FAKE,
+                                     FAKE, 2, None) == capi.BC_SUCCESS
 
 
 def test_commit_paths_rejects():

@@ -188,9 +188,10 @@ def test_large_batch_takes_split_path(oracle):
         assert np.all(err <= G.f16_tolerance(exp32, 2e-3)), f"ws={ws} max err {err.max():.3e}"
 
 
-def test_misaligned_workspace_runs_unsplit():
-    """A workspace that is not 16-byte aligned is ignored: the call gives the
-    same bits as the call without one."""
+def test_misaligned_workspace_is_ignored():
+    """A workspace that is not 16-byte aligned is ignored: the call is
+    bc_packed_decode's (whose split scratch is a slot of the library's pool)
+    and gives its bits."""
     torch.manual_seed(41)
     rng = np.random.default_rng(41)
     B, hq, hkv, d, NB = 4, 8, 2, 64, 300

@@ -217,9 +217,10 @@ def test_large_batches_pair_requests(case, oracle):
     _check(fix, oracle, atol=3e-4, what=f"B={len(case['lengths'])}")
 
 
-def test_misaligned_workspace_runs_single_pass():
-    """A workspace that is not 16-byte aligned is ignored: the call gives the
-    same bits as bc_tree_verify."""
+def test_misaligned_workspace_is_ignored():
+    """A workspace that is not 16-byte aligned is ignored: the call is
+    bc_tree_verify's (whose split scratch is a slot of the library's pool)
+    and gives its bits."""
     rng = np.random.default_rng(43)
     fix = oracle_np.tree_fixture(rng, 2, 600, 7, parents="random")
     k, v, pages, lengths, dq, dk, dv, par = fix
