@@ -585,7 +585,8 @@ void run_config(int n) {
     const double us = median_latency_us([&] { return gpu.launch(splits); });
     std::cout << "config " << n << " splits=" << splits << " max_abs_error=" << err << '\n';
     report("paged decode", us, decode_bytes(f, 4), c1, cn, cores);
-    if (!(err <= 2e-3f)) throw std::runtime_error("config parity failed");
+    // FP32 output: the reference driver's decode gate (src/main.cu:335).
+    if (!(err <= 3e-4f)) throw std::runtime_error("config parity failed");
   } else if (n == 2 || n == 3) {
     const int batch = n == 2 ? 1 : 8, prefix = n == 2 ? 2048 : 2053;
     TreeFixture t = make_tree_fixture(batch, prefix, 7, 128, 100 + n, 1.0f, true);
@@ -607,7 +608,8 @@ void run_config(int n) {
     std::cout << std::fixed << std::setprecision(3) << "expanded-prefix decode: " << e1
               << " us (splits 1), " << es << " us (splits " << splits << "); expanded/tree = "
               << std::min(e1, es) / us << "x\n";
-    if (!(err <= 2e-3f)) throw std::runtime_error("config parity failed");
+    // The reference driver's tree gate (src/main.cu:259).
+    if (!(err <= 3e-4f)) throw std::runtime_error("config parity failed");
   } else if (n == 5) {
     // [20000, 2, 16, 8, 128] cache, batch 64, contexts U[128, 4096]
     const int B = 64, NB = 20000, maxp = 256, hq = 32, hkv = 8, d = 128;
@@ -648,14 +650,21 @@ void run_config(int n) {
     CHECK(launch());
     CHECK(hipDeviceSynchronize());
     const auto out16 = dout.download<h16>();
-    float err = 0;
-    for (size_t i = 0; i < out16.size(); ++i)
-      err = std::max(err, std::fabs(oracle_h2f(out16[i]) - ref1[i]));
+    // FP16 output: the north star's 2e-3 plus half an FP16 ulp of the
+    // expected value (the output's own rounding).
+    float err = 0, excess = -1.f;
+    for (size_t i = 0; i < out16.size(); ++i) {
+      const float diff = std::fabs(oracle_h2f(out16[i]) - ref1[i]);
+      const uint16_t h = oracle_f2h(std::fabs(ref1[i]));
+      const float ulp = oracle_h2f((uint16_t)(h + 1)) - oracle_h2f(h);
+      err = std::max(err, diff);
+      excess = std::max(excess, diff - (2e-3f + 0.5f * ulp));
+    }
     const double us = median_latency_us(launch);
     Fixture geom{s, {}, {}, {}, {}, lens};
     std::cout << "config 5 max_abs_error(fp16 out vs fp32 oracle)=" << err << '\n';
     report("packed decode", us, decode_bytes(geom, 2), c1, cn, cores);
-    if (!(err <= 4e-3f)) throw std::runtime_error("config parity failed");
+    if (!(excess <= 0.f)) throw std::runtime_error("config parity failed");
   } else {
     throw std::runtime_error("config must be 1..5");
   }
