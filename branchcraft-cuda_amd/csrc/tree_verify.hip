@@ -646,37 +646,75 @@ __global__ __launch_bounds__(64 * W, 2) void tree_split_kernel(TreeParams P) {
   // Page ids of this wave's tiles as vector loads (lane j: page j%2 of the
   // wave's tile j/2, 32 tiles per register, the next 32 fetched a chunk
   // ahead).  Scalar loads would share lgkmcnt with the LDS reads of every
-  // tile, whose waits would then also wait for the prefetched ids.  The ids
-  // are requested with the length (they do not depend on it; entries past
-  // the wave's tiles or the prefix are unused).
+  // tile, whose waits would then also wait for the prefetched ids.
+  //
+  // Every load of the start is unconditional, from an address inside the
+  // request's table row (the page index clamped), and what the entry means
+  // is decided where it is used: a load under a condition is a branch, and
+  // after one the compiler's wait for the kernel arguments also waits for
+  // every scalar load in flight, which made the first two ids and the length
+  // three serial round trips ahead of the first Q and K/V loads.  The values
+  // that depend on the length are formed after those loads are issued.
   const int ntd = (P.nodes + kTile - 1) / kTile;  // draft tiles come first
+  const size_t prow = (size_t)b * P.max_pages;
+  auto table_entry = [&](int pg) { return P.pages[prow + min(max(pg, 0), P.max_pages - 1)]; };
+  // Raw entries of chunk `chunk` (ids_of keeps those that are ids).
   auto load_ids = [&](int chunk) {
     const int it = tbeg + ln + LN * (chunk * 32 + (lane >> 1));
-    const int pg = (it - ntd) * (kTile / BC_PAGE_SIZE) + (lane & 1);
-    return it < tbeg + T && pg >= 0 && pg < P.max_pages ? P.pages[(size_t)b * P.max_pages + pg]
-                                                         : -1;
+    return table_entry((it - ntd) * (kTile / BC_PAGE_SIZE) + (lane & 1));
   };
-  // Tile 0's ids as scalar loads: with the length they are all the first
-  // K/V loads wait for.
-  const int pg0 = (tbeg + ln - ntd) * (kTile / BC_PAGE_SIZE);
-  int cur[2] = {pg0 >= 0 && pg0 < P.max_pages ? P.pages[(size_t)b * P.max_pages + pg0] : -1,
-                pg0 >= 0 && pg0 + 1 < P.max_pages ? P.pages[(size_t)b * P.max_pages + pg0 + 1]
-                                                  : -1};
   int idv = load_ids(0);
-  int idv_next = -1;
-  if (T > 32 * LN) idv_next = load_ids(1);
-  const int len = max(0, min(P.lengths[b], P.max_pages * BC_PAGE_SIZE));
-  const int ntp = (len + kTile - 1) / kTile;
-  const int ntot = ntd + ntp;
-  const int tend = min(tbeg + T, ntot);
-  const int nmine =
-      present && tend > tbeg + ln ? (tend - tbeg - ln + LN - 1) / LN : 0;
+  int idv_next = load_ids(1);
 
   const int r = rt * 32 + lr;
   const bool rvalid = r < P.rows;
   const int rnode = div_by(r, P.group, P.group_mul);
   const int node = rvalid ? rnode : 0;
   const int h = kvh * P.group + (rvalid ? r - rnode * P.group : 0);
+
+  // Q stays in LDS (see s_q below) except in the D = 64 two-request
+  // workgroups.
+  constexpr bool QL = !(D == 64 && RQ == 2);
+  // Q^T fragments: with Q in LDS, the LN waves of a request load KS / LN of
+  // them each into s_q, so the workgroup fetches each fragment once instead
+  // of once per wave (every wave of a request reads the same rows).  Q and
+  // the parents load without selects (a select right after a load would wait
+  // for it there): lanes past the tile's query rows read row (node 0, head
+  // h), whose scores land in columns that are never written out, and parent
+  // entries past the node count repeat the last one and are never read
+  // (walks visit nodes in [0, nodes) only).
+  constexpr int QPW = QL ? (KS + LN - 1) / LN : KS;  // fragments loaded per wave
+  uint4 qown[QPW];
+  {
+    const uint16_t* qp = P.dq + (((size_t)b * P.nodes + node) * P.hq + h) * D + 8 * g;
+#pragma unroll
+    for (int j = 0; j < QPW; ++j)
+      qown[j] = ldg16(qp + 16 * (QL ? min(ln + LN * j, KS - 1) : j));
+  }
+
+  // A wave whose first tile is a draft tile (part 0's first waves: draft
+  // tiles come first) needs neither a page id nor the length for it, which
+  // the launch geometry alone tells; the other waves load tile 0's two
+  // entries and the length as scalar loads, together, after the vector loads
+  // above.  Only scalar loads sit under this condition: vector loads under a
+  // condition would leave the compiler's wait counts after it assuming the
+  // fewest either side issued.
+  const bool early = tbeg + ln < ntd;  // uniform
+  const int pg0 = (tbeg + ln - ntd) * (kTile / BC_PAGE_SIZE);
+  int raw0 = -1, raw1 = -1, len_raw = 0;
+  if (!early) {
+    raw0 = table_entry(pg0);
+    raw1 = table_entry(pg0 + 1);
+    len_raw = P.lengths[b];
+  }
+  int cur[2] = {-1, -1};
+  int len = 0, ntot = 0, nmine = 0;
+  auto set_lengths = [&]() {
+    len = max(0, min(len_raw, P.max_pages * BC_PAGE_SIZE));
+    ntot = ntd + (len + kTile - 1) / kTile;
+    const int tend = min(tbeg + T, ntot);
+    nmine = present && tend > tbeg + ln ? (tend - tbeg - ln + LN - 1) / LN : 0;
+  };
 
   __shared__ __attribute__((aligned(16))) _Float16 s_stage[W * STAGE];
   // Q^T B operand of each request's row tile: lane (g, lr) of k-step s
@@ -687,7 +725,6 @@ __global__ __launch_bounds__(64 * W, 2) void tree_split_kernel(TreeParams P) {
   // CU instead of two: there every wave holds it in registers.  The parent
   // array in registers: lane i holds parent[i + 64c] (c < 4), so a wave
   // walks ancestor chains with lane shuffles.
-  constexpr bool QL = !(D == 64 && RQ == 2);
   __shared__ uint4 s_q[QL ? RQ * KS * 64 : 1];
   uint4 qreg[QL ? 1 : KS];
   static_assert(BC_MAX_TREE_NODES <= 256, "four parent registers per lane");
@@ -736,13 +773,13 @@ __global__ __launch_bounds__(64 * W, 2) void tree_split_kernel(TreeParams P) {
         for (int j = 0; j < LPP; ++j) dst[q * LPP + j] = *reinterpret_cast<const uint4*>(src + loff[j]);
       }
     } else {
+      // Rows past the node count read the last node's row (masked); the
+      // clamp, unlike a select of addresses, keeps the loads branch-free.
       const uint16_t* src = is_v ? P.dv : P.dk;
 #pragma unroll
       for (int s = 0; s < KS; ++s) {
-        const int dn = (it + ntd) * kTile + s * RPI + lrow;
-        const size_t off =
-            dn < P.nodes ? (((size_t)b * P.nodes + dn) * P.hkv + kvh) * D + lcol : lcol;
-        dst[s] = ldg16(src + off);
+        const int dn = min((it + ntd) * kTile + s * RPI + lrow, P.nodes - 1);
+        dst[s] = ldg16(src + (((size_t)b * P.nodes + dn) * P.hkv + kvh) * D + lcol);
       }
     }
   };
@@ -788,7 +825,10 @@ __global__ __launch_bounds__(64 * W, 2) void tree_split_kernel(TreeParams P) {
     return is_draft ? ancestor_bits(parr, P.nodes, node, tbase)
                     : prefix_bits(len - tbase, ph[0], ph[1], P.phys_pages);
   };
-  auto process = [&](int idx, uint32_t okbits, const int (&next_ids)[2], auto first_tag) {
+  // staged: the tile's rows are in the staging area already (an early
+  // wave's first tile, see below).
+  auto process = [&](int idx, uint32_t okbits, const int (&next_ids)[2], auto first_tag,
+                     bool staged = false) {
     // Stage K and V rows; rows that are not valid tokens may hold any bits
     // (NaN included): their weight is zero, so their V row must be zero.
     auto stage_v = [&]() {
@@ -802,14 +842,16 @@ __global__ __launch_bounds__(64 * W, 2) void tree_split_kernel(TreeParams P) {
             *reinterpret_cast<uint4*>(vs + (s * RPI + lrow) * VP + lcol) = make_uint4(0, 0, 0, 0);
       }
     };
-#pragma unroll
-    for (int s = 0; s < KS; ++s)
-      *reinterpret_cast<uint4*>(ks + (s * RPI + lrow) * KP + lcol) = kreg[s];
-    // The first tile's scores start as soon as its K is staged (its V was
-    // issued after K and Q); later tiles stage both, then issue the next
-    // tile's loads, which are then in flight during this tile's MFMAs.
     constexpr bool first = decltype(first_tag)::value;
-    if (!first) stage_v();
+    if (!staged) {
+#pragma unroll
+      for (int s = 0; s < KS; ++s)
+        *reinterpret_cast<uint4*>(ks + (s * RPI + lrow) * KP + lcol) = kreg[s];
+      // The first tile's scores start as soon as its K is staged (its V was
+      // issued after K and Q); later tiles stage both, then issue the next
+      // tile's loads, which are then in flight during this tile's MFMAs.
+      if (!first) stage_v();
+    }
     wave_lds_sync();
     if (!first && idx + 1 < nmine) issue(idx + 1, next_ids);
     f16x8 pb[2], pl[2];
@@ -828,87 +870,109 @@ __global__ __launch_bounds__(64 * W, 2) void tree_split_kernel(TreeParams P) {
     wave_lds_sync();
   };
 
+  // Ids of the wave's tile idx < nmine: entries past the page table read as
+  // -1 (a draft tile's entries are never used).
   auto ids_of = [&](int idx, int (&ph)[2]) {
     if ((idx & 31) == 0 && idx > 0) {  // uniform: move to the next chunk of ids
       idv = idv_next;
       if (T > 32 * LN * ((idx >> 5) + 1)) idv_next = load_ids((idx >> 5) + 1);
     }
-    ph[0] = __builtin_amdgcn_readlane(idv, 2 * (idx & 31));
-    ph[1] = __builtin_amdgcn_readlane(idv, 2 * (idx & 31) + 1);
+    const int pg = (tbeg + ln + LN * idx - ntd) * (kTile / BC_PAGE_SIZE);
+    const int r0 = __builtin_amdgcn_readlane(idv, 2 * (idx & 31));
+    const int r1 = __builtin_amdgcn_readlane(idv, 2 * (idx & 31) + 1);
+    ph[0] = pg >= 0 && pg < P.max_pages ? r0 : -1;
+    ph[1] = pg >= 0 && pg + 1 < P.max_pages ? r1 : -1;
   };
-  // Tile 0's loads as one straight-line sequence for a draft and a prefix
-  // first tile alike (each load's address is selected per lane): after a
-  // branch with loads on both sides, the compiler's wait counts assume the
-  // fewest loads either side issued, so later waits would cover loads they
-  // need not wait for.  Pages outside the pool read page 0 and draft rows
-  // past the node count read row 0 (all in bounds); both are masked.
-  auto issue_first = [&](const int (&ph)[2], bool is_v) {
-    const int it = tbeg + ln - ntd;  // prefix tile index when >= 0
+  auto load_parents = [&]() {
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      parr[c] = P.parent[(size_t)b * P.nodes + min(lane + 64 * c, P.nodes - 1)];
+  };
+  // This wave's Q fragments into s_q.  Each path below writes them itself:
+  // the compiler's wait for Q at a point both paths reach is the stricter of
+  // the two, and it would make the later path wait for its whole first tile.
+  auto publish_q = [&]() {
+    if constexpr (QL) {
+#pragma unroll
+      for (int j = 0; j < QPW; ++j)
+        if (ln + LN * j < KS) s_q[((size_t)rq * KS + ln + LN * j) * 64 + lane] = qown[j];
+    }
+  };
+  // Tile 0's loads, one straight-line sequence for draft and prefix tiles
+  // alike (each address selected per wave): K, the parents, then V, so a
+  // prefix tile's scores wait for Q and K only.  A wave without tiles issues
+  // them too (pages outside the pool read page 0, draft rows past the node
+  // count the last node's row, all in bounds), so every wave runs the same
+  // loads and barriers.  Only a prefix tile's addresses wait for the scalar
+  // loads above; an early wave issues its draft tile's loads at once and
+  // stages the tile before the Q barrier, and after the barrier its first
+  // step issues the second tile's loads (in single passes over short
+  // prefixes this is the wave with the extra tile: one request over 256
+  // tokens has 9 tiles for 8 waves).
+  auto issue_first = [&](bool is_v) {
     uint4 (&dst)[KS] = is_v ? vreg : kreg;
     const uint16_t* pbase = is_v ? P.v : P.k;
     const uint16_t* dbase = is_v ? P.dv : P.dk;
-    // Draft row of load s: dn0 + s * RPI, each RPI rows dstep elements on.
-    const int dn0 = (it + ntd) * kTile + lrow;
-    const size_t dstep = (size_t)RPI * P.hkv * D;
-    const uint16_t* d0 = dbase + (((size_t)b * P.nodes + dn0) * P.hkv + kvh) * D + lcol;
+    const int dn0 = (tbeg + ln) * kTile + lrow;  // draft row of load 0 (early waves)
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
-      const bool okp = ph[q] >= 0 && ph[q] < P.phys_pages;
+      const bool okp = cur[q] >= 0 && cur[q] < P.phys_pages;
       const char* pg = reinterpret_cast<const char*>(
-          pbase + (size_t)(okp ? ph[q] : 0) * page_elems + (size_t)kvh * D);
+          pbase + (size_t)(okp ? cur[q] : 0) * page_elems + (size_t)kvh * D);
 #pragma unroll
       for (int j = 0; j < LPP; ++j) {
         const int s = q * LPP + j;
-        const uint16_t* da = dn0 + s * RPI < P.nodes ? d0 + s * dstep : dbase + lcol;
-        const uint4* src = it >= 0 ? reinterpret_cast<const uint4*>(pg + loff[j])
-                                   : reinterpret_cast<const uint4*>(da);
-        dst[s] = *src;
+        const int dn = min(dn0 + s * RPI, P.nodes - 1);
+        const uint16_t* da = dbase + (((size_t)b * P.nodes + dn) * P.hkv + kvh) * D + lcol;
+        dst[s] = *(early ? reinterpret_cast<const uint4*>(da)
+                         : reinterpret_cast<const uint4*>(pg + loff[j]));
       }
     }
   };
-  // Load order: this wave's share of Q, tile 0's K, the parents, tile 0's V,
-  // so the first scores wait for Q, K and the parents only.  A wave without
-  // tiles issues tile 0's loads too (its addresses stay inside the tensors),
-  // so every wave runs the same loads and barriers.  Q and the parents load
-  // without selects (a select right after a load would wait for it there):
-  // lanes past the tile's query rows read row (node 0, head h), whose scores
-  // land in columns that are never written out, and parent entries past the
-  // node count repeat the last one and are never read (walks visit nodes in
-  // [0, nodes) only).
-  //
-  // Q^T fragments: with Q in LDS, the LN waves of a request load KS / LN of
-  // them each into s_q, so the workgroup fetches each fragment once instead
-  // of once per wave (every wave of a request reads the same rows).
-  constexpr int QPW = QL ? (KS + LN - 1) / LN : KS;  // fragments loaded per wave
-  uint4 qown[QPW];
-  {
-    const uint16_t* qp = P.dq + (((size_t)b * P.nodes + node) * P.hq + h) * D + 8 * g;
-#pragma unroll
-    for (int j = 0; j < QPW; ++j)
-      qown[j] = ldg16(qp + 16 * (QL ? min(ln + LN * j, KS - 1) : j));
+  __builtin_amdgcn_sched_barrier(0);  // Q's loads go out before the id wait
+  if (!early) {
+    cur[0] = pg0 >= 0 && pg0 < P.max_pages ? raw0 : -1;
+    cur[1] = pg0 >= 0 && pg0 + 1 < P.max_pages ? raw1 : -1;
   }
-  issue_first(cur, false);
+  issue_first(false);
+  load_parents();
+  issue_first(true);
+  publish_q();
+  if (early) {
+    // The draft tile's rows into the staging area (V rows that are not
+    // tokens zeroed by a mask), then the length.  No vector load is issued
+    // here: the waits after this block are then exactly the other path's
+    // (issuing the second tile here made that path's first K wait also
+    // cover most of its V).
+    rowok = rows_of(0, cur);
 #pragma unroll
-  for (int c = 0; c < 4; ++c)
-    parr[c] = P.parent[(size_t)b * P.nodes + min(lane + 64 * c, P.nodes - 1)];
-  issue_first(cur, true);
+    for (int s = 0; s < KS; ++s) {
+      const unsigned keep = 0u - ((rowok >> s) & 1u);
+      *reinterpret_cast<uint4*>(ks + (s * RPI + lrow) * KP + lcol) = kreg[s];
+      *reinterpret_cast<uint4*>(vs + (s * RPI + lrow) * VP + lcol) =
+          make_uint4(vreg[s].x & keep, vreg[s].y & keep, vreg[s].z & keep, vreg[s].w & keep);
+    }
+    len_raw = P.lengths[b];
+  }
+  set_lengths();
   rowok = rows_of(0, cur);
   if constexpr (QL) {
-#pragma unroll
-    for (int j = 0; j < QPW; ++j)
-      if (ln + LN * j < KS) s_q[((size_t)rq * KS + ln + LN * j) * 64 + lane] = qown[j];
     __syncthreads();  // every wave's Q fragments are in s_q
   } else {
 #pragma unroll
     for (int j = 0; j < KS; ++j) qreg[j] = qown[j];
   }
-  if (nmine > 0) {
+  if (nmine > 0 && !early) {
     int nxt[2] = {-1, -1};
     if (1 < nmine) ids_of(1, nxt);
-    process(0, okbits_of(0, cur, tbeg + ln < ntd), nxt, std::true_type{});
+    process(0, okbits_of(0, cur, false), nxt, std::true_type{});
     cur[0] = nxt[0];
     cur[1] = nxt[1];
   } else {
+    // No tile yet, or an early wave's staged first tile, which the loop
+    // below takes with the later tiles' code from acc = 0, m = -inf, l = 0:
+    // the rescale then multiplies zeros by 0, and the result is the
+    // first-tile code's bit for bit.
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
@@ -916,10 +980,11 @@ __global__ __launch_bounds__(64 * W, 2) void tree_split_kernel(TreeParams P) {
   }
   // The loads run one tile ahead of the MFMAs: while tile idx is processed,
   // tile idx+1's rows are loading.
-  for (int idx = 1; idx < nmine; ++idx) {
+  for (int idx = early ? 0 : 1; idx < nmine; ++idx) {
     int nxt[2] = {-1, -1};
     if (idx + 1 < nmine) ids_of(idx + 1, nxt);
-    process(idx, okbits_of(idx, cur, tbeg + ln + LN * idx < ntd), nxt, std::false_type{});
+    process(idx, okbits_of(idx, cur, tbeg + ln + LN * idx < ntd), nxt, std::false_type{},
+            early && idx == 0);
     cur[0] = nxt[0];
     cur[1] = nxt[1];
   }
