@@ -81,6 +81,19 @@ struct AttnParams {
                           // waves splitting the pages (merged through LDS)
 };
 
+// Every kernel argument into scalar registers at the kernel's start, in one
+// round of loads.  Otherwise the compiler loads each field where it is first
+// used, and a field first used after a branch costs one more serial round
+// trip before the kernel's first memory access.
+__device__ __forceinline__ void pin_params(const AttnParams& P) {
+  asm volatile("" ::"s"(P.q), "s"(P.kbase), "s"(P.vbase), "s"(P.pages), "s"(P.lengths),
+               "s"(P.out), "s"(P.part_acc), "s"(P.part_ml), "s"(P.page_stride),
+               "s"(P.head_stride), "s"(P.slot_stride), "s"(P.batch), "s"(P.hq), "s"(P.hkv),
+               "s"(P.group), "s"(P.nblk), "s"(P.max_pages), "s"(P.phys_pages), "s"(P.zdim),
+               "s"(P.waves), "s"(P.scale_log2), "s"(P.nwg));
+  __builtin_amdgcn_sched_barrier(0);  // nothing that uses them moves above
+}
+
 __device__ __forceinline__ int seq_len(const AttnParams& P, int b) {
   return max(0, min(P.lengths[b], P.max_pages * BC_PAGE_SIZE));
 }
@@ -201,6 +214,7 @@ __device__ __forceinline__ void wave_lds_sync() {
 template <int D, typename OutT, bool VEC, int WAVES>
 __global__ __launch_bounds__(64 * WAVES, WAVES == kMaxWaves ? 3 : 2) void paged_attn_kernel(
     AttnParams P) {
+  pin_params(P);
   constexpr int KS = D / 32;   // QK k-steps (and 16-byte loads per page row set)
   constexpr int DT = D / 16;   // 16-dim output tiles
   constexpr int VP = D + 16;   // halves per staged V row
@@ -521,6 +535,7 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == kMaxWaves ? 3 : 2) void paged_
 // hundreds of partials, too many for one wave.
 template <int D, typename OutT, int RW>
 __global__ __launch_bounds__(256) void merge_kernel(AttnParams P) {
+  pin_params(P);
   static_assert(RW == 1 || RW == 4, "one or four waves per row");
   constexpr int PER = D / 64;
   const int lane = threadIdx.x & 63;

@@ -80,6 +80,20 @@ struct TreeParams {
   int grid3d;
 };
 
+// Every kernel argument into scalar registers at the kernel's start, in one
+// round of loads.  Otherwise the compiler loads each field where it is first
+// used, and a field first used after a branch costs one more serial round
+// trip before the kernel's first memory access.
+__device__ __forceinline__ void pin_params(const TreeParams& P) {
+  asm volatile("" ::"s"(P.k), "s"(P.v), "s"(P.pages), "s"(P.lengths), "s"(P.dq), "s"(P.dk),
+               "s"(P.dv), "s"(P.parent), "s"(P.out), "s"(P.part_acc), "s"(P.part_ml),
+               "s"(P.batch), "s"(P.nodes), "s"(P.hq), "s"(P.hkv), "s"(P.group),
+               "s"(P.max_pages), "s"(P.phys_pages), "s"(P.rows), "s"(P.row_tiles),
+               "s"(P.scale_log2), "s"(P.parts), "s"(P.tiles_per_part), "s"(P.group_mul),
+               "s"(P.rt_mul), "s"(P.grid3d));
+  __builtin_amdgcn_sched_barrier(0);  // nothing that uses them moves above
+}
+
 // n / d, as a multiply-high when the host passed mul = ceil(2^32 / d) (exact
 // for n * d < 2^32, which the host checks), else a plain division.
 __device__ __forceinline__ int div_by(int n, int d, unsigned long long mul) {
@@ -100,6 +114,7 @@ __device__ __forceinline__ f16x4 lds_read_tr(const _Float16* p) {
 
 template <int D, bool VEC>
 __global__ __launch_bounds__(kThreads, 2) void tree_kernel(TreeParams P) {
+  pin_params(P);
   constexpr int KS = D / 16;  // MFMA k-steps over the head dimension
   constexpr int DT = D / 32;  // 32-row output tiles over the head dimension
   constexpr int VP = v_pitch<D>();
@@ -611,6 +626,7 @@ __global__ __launch_bounds__(64 * W, 2) void tree_split_kernel(TreeParams P) {
   constexpr int STAGE = kTile * (KP + VP);  // halves per wave
   constexpr int LN = W / RQ;      // waves per request
 
+  pin_params(P);
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int g = lane >> 5;   // lane half
@@ -1077,6 +1093,7 @@ __global__ __launch_bounds__(64 * W, 2) void tree_split_kernel(TreeParams P) {
 // rest eight slots at a time.
 template <int D, int NB>
 __global__ __launch_bounds__(256) void merge_split_kernel(TreeParams P) {
+  pin_params(P);
   constexpr int PER = D / 64;
   constexpr int NS = 8 * NB;  // slots loaded in the first round
   const int lane = threadIdx.x & 63;
@@ -1160,6 +1177,7 @@ void launch_merge_split(const TreeParams& P, dim3 grid, hipStream_t st) {
 // those of tree_kernel.
 template <int D, bool VEC>
 __global__ __launch_bounds__(kThreads, 2) void tree_rows_kernel(TreeParams P) {
+  pin_params(P);
   constexpr int KS = D / 16;
   constexpr int DT = D / 32;
   constexpr int VP = v_pitch<D>();
