@@ -152,3 +152,21 @@ def compile_device_asm(source: Path, out_dir: Path) -> str:
            "--cuda-device-only", "-S", str(source), "-o", str(out)]
     subprocess.run(cmd, check=True, capture_output=True, text=True)
     return out.read_text()
+
+
+def kernarg_rounds(lines: list[str]) -> list[int]:
+    """Kernel-argument loads (`s_load*` from the kernarg pointer s[0:1]) issued
+    before the kernel's first vector-memory load, grouped by the scalar waits
+    between them: [3] is one round of three loads, [1, 2] two serial rounds."""
+    groups, cur = [], 0
+    for op, args in parse(lines)[0]:
+        if op.startswith("s_load") and "s[0:1]" in args:
+            cur += 1
+        elif op == "s_waitcnt" and "lgkmcnt" in args and cur:
+            groups.append(cur)
+            cur = 0
+        elif op.startswith(("global_load", "buffer_load", "flat_load")):
+            break
+    if cur:
+        groups.append(cur)
+    return groups

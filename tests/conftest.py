@@ -22,6 +22,20 @@ def pytest_configure(config):
 
 
 @pytest.fixture(scope="session")
+def compiled_kernels(tmp_path_factory):
+    """gfx950 device assembly of decode.hip and tree_verify.hip, built with
+    the library's flags: {source: {kernel symbol: lines}}."""
+    import shutil
+
+    import asm_hazards as H
+    if not (shutil.which("hipcc") or Path("/opt/rocm/bin/hipcc").exists()):
+        pytest.skip("hipcc not available")
+    tmp = tmp_path_factory.mktemp("asm")
+    return {src: H.kernels(H.compile_device_asm(H.CSRC / src, tmp))
+            for src in ("decode.hip", "tree_verify.hip")}
+
+
+@pytest.fixture(scope="session")
 def oracle():
     from oracle import oracle_c
     oracle_c.lib()

@@ -25,15 +25,10 @@ the failing sequence above must read as 3 wait states, padded sequences as
 their padding.
 """
 
-import shutil
-import tempfile
-from pathlib import Path
-
 import pytest
 
 import asm_hazards as H
 
-ROOT = Path(__file__).resolve().parent.parent
 MARGIN = 10  # fewest wait states any passing build had (the failing ones: 3)
 
 
@@ -79,21 +74,10 @@ def test_checker_counts_nops_branches_and_kills():
     assert "WARC" not in _scan_text(killed)  # v12 was reloaded before the write
 
 
-@pytest.fixture(scope="module")
-def compiled():
-    if not (shutil.which("hipcc") or Path("/opt/rocm/bin/hipcc").exists()):
-        pytest.skip("hipcc not available")
-    out = {}
-    with tempfile.TemporaryDirectory() as tmp:
-        for src in ("decode.hip", "tree_verify.hip"):
-            out[src] = H.kernels(H.compile_device_asm(H.CSRC / src, Path(tmp)))
-    return out
-
-
 @pytest.mark.parametrize("src", ["decode.hip", "tree_verify.hip"])
-def test_shipped_kernels_keep_the_margin(compiled, src):
+def test_shipped_kernels_keep_the_margin(compiled_kernels, src):
     found_mfma = 0
-    for name, lines in compiled[src].items():
+    for name, lines in compiled_kernels[src].items():
         insts, labels = H.parse(lines)
         if not any(op.startswith("v_mfma") for op, _ in insts):
             continue

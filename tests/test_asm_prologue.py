@@ -1,0 +1,49 @@
+"""Every shipped kernel loads all its kernel arguments in one round.
+
+Left to itself, the compiler loads each parameter field where it is first
+used; fields first used after a branch then cost a second and third serial
+scalar round trip before the kernel's first memory access (every kernel here
+had two or three).  Each kernel now reads all its fields at entry (an empty
+asm that takes them in scalar registers, then a scheduling barrier), and
+this test holds the compiled gfx950 code to one round.  The checker is
+pinned by planted assembly.
+"""
+
+import pytest
+
+import asm_hazards as H
+
+
+def _rounds(text: str) -> list[int]:
+    return H.kernarg_rounds(text.strip().split("\n"))
+
+
+def test_checker_counts_rounds():
+    one = """
+\ts_load_dwordx16 s[8:23], s[0:1], 0x0
+\ts_load_dwordx4 s[24:27], s[0:1], 0x40
+\ts_waitcnt lgkmcnt(0)
+\ts_load_dword s30, s[10:11], 0x0
+\ts_waitcnt lgkmcnt(0)
+\tglobal_load_dword v1, v0, s[12:13]
+\ts_load_dword s31, s[0:1], 0x80
+"""
+    assert _rounds(one) == [2]  # loads from other bases and after the first VMEM do not count
+    two = """
+\ts_load_dwordx8 s[36:43], s[0:1], 0x58
+\ts_waitcnt lgkmcnt(0)
+\ts_cbranch_scc1 .LBB0_2
+\ts_load_dwordx2 s[52:53], s[0:1], 0x50
+\ts_load_dwordx4 s[48:51], s[0:1], 0x40
+\ts_waitcnt lgkmcnt(0)
+\tglobal_load_dword v1, v0, s[48:49]
+"""
+    assert _rounds(two) == [1, 2]
+
+
+@pytest.mark.parametrize("src", ["decode.hip", "tree_verify.hip"])
+def test_kernel_arguments_load_in_one_round(compiled_kernels, src):
+    kernels = compiled_kernels[src]
+    assert len(kernels) >= 10, f"{src}: expected the kernel instances, found {len(kernels)}"
+    for name, lines in kernels.items():
+        assert len(H.kernarg_rounds(lines)) == 1, (name, H.kernarg_rounds(lines))
