@@ -1,12 +1,12 @@
-"""Every shipped kernel loads all its kernel arguments in one round.
+"""The shipped kernels load all their kernel arguments in one round.
 
 Left to itself, the compiler loads each parameter field where it is first
 used; fields first used after a branch then cost a second and third serial
 scalar round trip before the kernel's first memory access (every kernel here
 had two or three).  Each kernel now reads all its fields at entry (an empty
 asm that takes them in scalar registers, then a scheduling barrier), and
-this test holds the compiled gfx950 code to one round.  The checker is
-pinned by planted assembly.
+this test holds the compiled gfx950 code to one round, except the kernel
+listed in EXEMPT.  The checker is pinned by planted assembly.
 """
 
 import pytest
@@ -41,9 +41,20 @@ def test_checker_counts_rounds():
     assert _rounds(two) == [1, 2]
 
 
+# tree_rows_kernel runs tens to hundreds of microseconds per launch; pinning
+# its arguments measured 0.4-2 % slower there, against about 0.5 us saved at
+# the start, so it keeps the compiler's placement.
+EXEMPT = ("tree_rows_kernel",)
+
+
 @pytest.mark.parametrize("src", ["decode.hip", "tree_verify.hip"])
 def test_kernel_arguments_load_in_one_round(compiled_kernels, src):
     kernels = compiled_kernels[src]
     assert len(kernels) >= 10, f"{src}: expected the kernel instances, found {len(kernels)}"
+    checked = 0
     for name, lines in kernels.items():
+        if any(e in name for e in EXEMPT):
+            continue
         assert len(H.kernarg_rounds(lines)) == 1, (name, H.kernarg_rounds(lines))
+        checked += 1
+    assert checked >= 10
