@@ -52,8 +52,8 @@ typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef short i16x4 __attribute__((ext_vector_type(4)));
 
-// Four waves per workgroup at <= 168 VGPRs: up to three workgroups share a
-// CU, so a CU keeps 8-12 waves of page loads in flight.
+// Up to four waves per workgroup at <= 168 VGPRs (three such workgroups fit
+// a CU).  Flat ranges launch one wave of workgroups, four waves per CU.
 constexpr int kMaxWaves = 4;
 // Waves per workgroup without a workspace: one (sequence, head block) per
 // workgroup, the pages split kSlices ways and merged through LDS.
@@ -67,7 +67,7 @@ struct AttnParams {
   const int32_t* pages;   // [B, max_pages]
   const int32_t* lengths; // [B]
   void* out;              // [B, Hq, D], float or _Float16
-  float* part_acc;        // partials [slot][Hq][D], slot = workgroup + sequence
+  float* part_acc;        // partials [slot][Hq][D] (slot: see pair_slots)
   float* part_ml;         // partials [slot][Hq][2]: (max in log2 units, sum)
   long long page_stride;  // elements between physical pages
   long long head_stride;  // elements between KV heads
@@ -79,6 +79,10 @@ struct AttnParams {
   int nwg;                // > 0: flat page ranges over nwg workgroups;
                           // 0: one workgroup per (sequence, head block), its
                           // waves splitting the pages (merged through LDS)
+  int pair_slots;         // partial slot of range r cutting sequence b:
+                          // 0: r + b (nwg + batch slots); 1: 2r for the
+                          // range's first sequence, 2r + 1 for a later one
+                          // (2 * nwg slots, for batches above nwg)
 };
 
 // Every kernel argument into scalar registers at the kernel's start, in one
@@ -90,7 +94,7 @@ __device__ __forceinline__ void pin_params(const AttnParams& P) {
                "s"(P.out), "s"(P.part_acc), "s"(P.part_ml), "s"(P.page_stride),
                "s"(P.head_stride), "s"(P.slot_stride), "s"(P.batch), "s"(P.hq), "s"(P.hkv),
                "s"(P.group), "s"(P.nblk), "s"(P.max_pages), "s"(P.phys_pages), "s"(P.zdim),
-               "s"(P.waves), "s"(P.scale_log2), "s"(P.nwg));
+               "s"(P.waves), "s"(P.scale_log2), "s"(P.nwg), "s"(P.pair_slots));
   __builtin_amdgcn_sched_barrier(0);  // nothing that uses them moves above
 }
 
@@ -264,6 +268,7 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == kMaxWaves ? 3 : 2) void paged_
   }
   int ppages = pages_of(plen);
   int seg0 = plocal;  // first local page of pb in this range
+  const int pb_first = pb;  // the range's first sequence
 
   // Q^T B operand: lane holds Q[head h0+c16][32s + 8*g4 .. +8].
   uint4 qB[KS];
@@ -294,7 +299,10 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == kMaxWaves ? 3 : 2) void paged_
         store4<OutT, VEC>(P.out, o + 16 * t, acc[t][0] * inv, acc[t][1] * inv,
                           acc[t][2] * inv, acc[t][3] * inv);
     } else {
-      const size_t r = (size_t)(rid + pb) * P.hq + h;
+      // A range cuts at most two sequences: its first (which started in an
+      // earlier range) and its last (which goes on in the next one).
+      const int slot = P.pair_slots ? 2 * rid + (pb != pb_first ? 1 : 0) : rid + pb;
+      const size_t r = (size_t)slot * P.hq + h;
       float* pa = P.part_acc + r * D + 4 * g4;
 #pragma unroll
       for (int t = 0; t < DT; ++t)
@@ -566,6 +574,11 @@ __global__ __launch_bounds__(256) void merge_kernel(AttnParams P) {
   const int per = (total + P.nwg - 1) / P.nwg;
   const int w0 = before / per, w1 = (before + np - 1) / per;
   if (w0 == w1) return;  // the sequence ended inside one range: written directly
+  // Range w's partial slot (AttnParams::pair_slots).  With pair slots, b is
+  // the first sequence of every range w0 < w <= w1 (they start on its
+  // pages), and of range w0 only if w0 starts on b's first page.
+  const int w0_off = P.pair_slots && w0 * per < before ? 1 : 0;
+  auto slot_of = [&](int w) { return P.pair_slots ? 2 * w + (w == w0 ? w0_off : 0) : w + b; };
   // This wave's partials: [r0, r1] (empty when r1 < r0).
   const int nparts = w1 - w0 + 1;
   const int r0 = w0 + sub * nparts / RW, r1 = w0 + (sub + 1) * nparts / RW - 1;
@@ -578,7 +591,7 @@ __global__ __launch_bounds__(256) void merge_kernel(AttnParams P) {
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
       const int i = min(i0 + u, cnt - 1);
-      const float* src = P.part_acc + ((size_t)(wb + i + b) * P.hq + h) * D + lane;
+      const float* src = P.part_acc + ((size_t)slot_of(wb + i) * P.hq + h) * D + lane;
 #pragma unroll
       for (int j = 0; j < PER; ++j) v[u][j] = src[64 * j];
     }
@@ -587,7 +600,7 @@ __global__ __launch_bounds__(256) void merge_kernel(AttnParams P) {
     const int cnt = min(64, r1 - wb + 1);
     // The (max, sum) loads and the first step's partials go out together:
     // the partial loads do not depend on the weights.
-    const size_t r = (size_t)(wb + min(lane, cnt - 1) + b) * P.hq + h;
+    const size_t r = (size_t)slot_of(wb + min(lane, cnt - 1)) * P.hq + h;
     const float mp0 = P.part_ml[2 * r], lp0 = P.part_ml[2 * r + 1];
     float v[8][PER];
     load8p(wb, cnt, 0, v);
@@ -710,33 +723,43 @@ hipError_t launch(AttnParams& P, int dim, hipStream_t st) {
 
 using bch::device_cus;
 
-// Flat-mode workgroup count for a given number of partial slots per head:
-// slot = workgroup + sequence must stay below `slots`, and a whole number of
-// waves of workgroups over the CUs balances best.
-int flat_workgroups(int batch, long long slots, int cus, int zgroups) {
+long long zdim_of(const bc_shape& s) {
+  const int group = s.query_heads / s.kv_heads;
+  return (long long)s.kv_heads * ((group + kHeadCols - 1) / kHeadCols);
+}
+
+// Flat ranges for one wave of workgroups: each range runs one wave per head
+// block (zdim waves), and kMaxWaves waves per CU keep the most bytes in
+// flight (same box, 32/8 heads: one wave more per SIMD measured 5 % slower
+// at 64 sequences; at 1-2 head blocks, one workgroup per CU left the CUs
+// 16-45 % slower than four waves each).
+int flat_ranges(const bc_shape& s, int cus) {
+  const long long n = (long long)(cus > 0 ? cus : 256) * kMaxWaves / zdim_of(s);
+  return n < 1 ? 1 : n > (1 << 20) ? (1 << 20) : (int)n;
+}
+
+// Flat-mode workgroup count for bc_decode's `slots` partial slots per head:
+// slot = workgroup + sequence must stay below `slots`, and more ranges than
+// one wave of workgroups only add partials (one wave: 85.9 us against 103.8
+// us for 64 sequences of up to 4096 tokens at 16 splits).
+int flat_workgroups(int batch, long long slots, int ranges) {
   long long nwg = slots - batch + 1;
-  const long long per_wave = cus / (zgroups > 0 ? zgroups : 1);
-  if (per_wave >= 1 && nwg > per_wave) nwg = nwg / per_wave * per_wave;
+  if (nwg > ranges) nwg = ranges;
   if (nwg < 1) nwg = 1;
   return (int)nwg;
 }
 
-int zgroups_of(const bc_shape& s) {
-  const int group = s.query_heads / s.kv_heads;
-  const int zdim = s.kv_heads * ((group + kHeadCols - 1) / kHeadCols);
-  const int waves = zdim < kMaxWaves ? zdim : kMaxWaves;
-  return (zdim + waves - 1) / waves;
-}
+// Packed decode with a workspace: one wave of flat ranges.
+int packed_nwg(const bc_shape& s) { return flat_ranges(s, device_cus()); }
 
-// Packed decode with a workspace: flat ranges over one workgroup per CU.
-int packed_nwg(const bc_shape& s) {
-  const int zg = zgroups_of(s);
-  int n = device_cus() / zg;
-  return n < 1 ? 1 : n;
+// Partial slots per head: nwg + batch with slot = range + sequence, or two
+// per range once the batch outnumbers the ranges (AttnParams::pair_slots).
+size_t packed_slots(const bc_shape& s, int nwg) {
+  return s.batch > nwg ? 2 * (size_t)nwg : (size_t)nwg + s.batch;
 }
 
 size_t packed_workspace(const bc_shape& s, int nwg) {
-  const size_t slots = (size_t)nwg + s.batch;
+  const size_t slots = packed_slots(s, nwg);
   const size_t acc = (slots * s.query_heads * s.dim * sizeof(float) + 255) & ~(size_t)255;
   return acc + slots * s.query_heads * 2 * sizeof(float);
 }
@@ -770,42 +793,44 @@ extern "C" int bc_decode(bc_shape s, bc_inputs in, bc_scratch scratch,
   // splits == 1: one workgroup per sequence.  splits > 1: flat ranges whose
   // partial slots fit the caller's splits*B*Hq rows.
   P.nwg = splits == 1 ? 0
-                      : flat_workgroups(s.batch, (long long)splits * s.batch, device_cus(),
-                                        zgroups_of(s));
+                      : flat_workgroups(s.batch, (long long)splits * s.batch,
+                                        flat_ranges(s, device_cus()));
   return launch<float>(P, s.dim, reinterpret_cast<hipStream_t>(stream));
 }
 
 extern "C" int bc_auto_splits(bc_shape s, int max_length, int cu_count) {
   // splits == 1 runs one workgroup per (sequence, head block) with the pages
-  // split kSlices ways inside it and no merge kernel: the faster choice while
-  // every slice is short (contexts up to 768 tokens, or 1024 for batches
-  // that fill half the CUs or more) and those workgroups fit the CUs at once.  Otherwise split decode runs flat page ranges: (splits -
-  // 1) * batch + 1 of them, rounded down to whole waves of one workgroup per
-  // CU.  Pick the smallest split count that reaches a full wave, so that no CU
-  // idles: at batch 64 two splits would leave 65 of 128 ranges (55 % of HBM
-  // bandwidth), three fill them (76 %).  Batches of one to two waves take two
-  // splits (128 sequences of up to 4096 tokens: 80 % against 70 % unsplit);
-  // larger batches keep one workgroup per (sequence, head block), which
-  // measured faster at 512 sequences of up to 1024 tokens.
+  // split kSlices ways inside it and no merge kernel.  splits > 1 runs flat
+  // page ranges, min((splits - 1) * batch + 1, R) of them, R = flat_ranges
+  // (one wave of workgroups at four waves per CU).
+  //  - Batches of R sequences or more take two splits, so R ranges, whatever
+  //    the context length: one wave of workgroups streaming many sequences
+  //    each beats a launch of one workgroup per (sequence, head block) in
+  //    rounds (same box, 32/8 heads, R = 128: 384 sequences of up to 1024
+  //    tokens 151.5 against 161.3 us, 512 of up to 256 tokens 68.5 against
+  //    86.9 us, 2048 of up to 128 tokens 246.8 against 276.8 us).
+  //  - Smaller batches keep the reference's rule that contexts below 512
+  //    tokens stay whole (src/paged_gqa.cu:135), and stay whole up to 768
+  //    tokens (1024 where their workgroups fill half the CUs or more) while
+  //    those workgroups fit the CUs at once.
+  //  - Otherwise the smallest split count whose ranges fill the wave, so
+  //    that no CU idles: at batch 64 two splits would leave 65 of 128 ranges
+  //    (55 % of HBM bandwidth), three fill them (76 %).
   if (s.batch < 1 || s.kv_heads < 1 || s.query_heads < 1 || s.query_heads % s.kv_heads)
     return 1;
-  // Contexts below 512 tokens never split (src/paged_gqa.cu:135): a merge
-  // launch costs more than the few pages a split would spread.
-  if (max_length < 512) return 1;
   const int cus = cu_count > 0 ? cu_count : 256;
-  const int group = s.query_heads / s.kv_heads;
-  const long long zdim = (long long)s.kv_heads * ((group + kHeadCols - 1) / kHeadCols);
+  const int ranges = flat_ranges(s, cus);
+  if (ranges <= 1) return 1;
+  if (s.batch >= ranges) return 2;
+  if (max_length < 512) return 1;
   // Unsplit up to 768 tokens; up to 1024 only where the batch's workgroups
   // already fill half the CUs or more (1024 tokens, 32/8 heads, same box:
   // one sequence 12.3 us unsplit against 9.7 us split, 8 sequences 14.4
   // against 12.7, 12 sequences 16.0 against 16.0, 16 sequences 17.0 against
   // 18.0, 32 sequences 23.5 against 24.9 at the best split count).
-  const long long wgs = (long long)s.batch * zdim;
+  const long long wgs = (long long)s.batch * zdim_of(s);
   if (wgs <= cus && (max_length <= 768 || (max_length <= 1024 && 2 * wgs >= cus))) return 1;
-  const int per_wave = cus / zgroups_of(s);
-  if (per_wave <= 1) return 1;
-  if (s.batch >= per_wave) return s.batch <= 2 * per_wave ? 2 : 1;
-  long long splits = ((long long)per_wave + 2LL * s.batch - 2) / s.batch;
+  long long splits = ((long long)ranges + 2LL * s.batch - 2) / s.batch;
   if (splits > BC_MAX_SPLITS) splits = BC_MAX_SPLITS;
   return (int)splits;
 }
@@ -861,7 +886,8 @@ static int packed_common(bc_shape s, const bc_half* q, const bc_half* kv,
   const size_t need = packed_workspace(s, nwg);
   if (ws && ws_bytes >= need && aligned16(ws) && packed_split(s)) {
     P.nwg = nwg;
-    const size_t slots = (size_t)nwg + s.batch;
+    P.pair_slots = s.batch > nwg ? 1 : 0;
+    const size_t slots = packed_slots(s, nwg);
     const size_t acc_bytes =
         (slots * s.query_heads * s.dim * sizeof(float) + 255) & ~(size_t)255;
     P.part_acc = static_cast<float*>(ws);

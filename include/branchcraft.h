@@ -112,7 +112,8 @@ typedef struct bc_tree_inputs {
 /* Paged GQA decode.  splits == 1 runs one workgroup per (sequence, head
  * block), its waves splitting the pages and merging in LDS, with no scratch.
  * splits > 1 spreads the batch's pages over equal ranges of the concatenated
- * sequences, at most (splits - 1) * B + 1 workgroups, and merges the FP32
+ * sequences, at most (splits - 1) * B + 1 of them and at most one wave of
+ * workgroups (4 * CUs / head blocks ranges), and merges the FP32
  * partial softmax states of the sequences a range boundary cuts; the
  * partials fit the reference's scratch sizes for `splits`.  FP16 tensors
  * that are not 16-byte aligned are read with 2-byte loads.
@@ -124,7 +125,10 @@ int bc_decode(bc_shape shape, bc_inputs in, bc_scratch scratch, int splits,
               bc_stream_t stream);
 
 /* Split-count heuristic for bc_decode on a device with `cu_count` compute
- * units; returns a value in [1, BC_MAX_SPLITS], 1 for max_length < 512.
+ * units; returns a value in [1, BC_MAX_SPLITS]: 2 for batches of at least
+ * one wave of flat ranges (4 * cu_count / head blocks: 128 sequences at 8
+ * KV heads of 4 query heads on 256 CUs) at any length, else 1 for
+ * max_length < 512.
  * Replaces branchcraft::auto_splits, include/branchcraft.hpp:41
  * (src/paged_gqa.cu:134-142), retuned for 256-CU MI355X workgroups: unlike
  * the reference (at most 16) it may return more than 16 (33 for 4
@@ -234,17 +238,19 @@ int bc_packed_decode(bc_shape shape, const bc_half* q, const bc_half* packed_kv,
                      long long head_stride, long long slot_stride,
                      long long kv_stride, float scale, bc_stream_t stream);
 
-/* Bytes of workspace bc_packed_decode_ws needs for this shape.  0 when
- * bc_auto_splits, given the table's capacity (max_pages * 16 tokens), keeps
- * the shape unsplit: a table under 512 tokens; one of at most 768 tokens
- * whose (sequence, head block) workgroups fit the CUs, or of at most 1024
- * tokens whose workgroups fill half the CUs or more; or a batch above two
- * waves of flat ranges (256 sequences at 8 KV heads on 256 CUs).  Such calls run unsplit, with no
- * merge, whatever workspace is passed. */
+/* Bytes of workspace bc_packed_decode_ws needs for this shape: FP32
+ * partials of min(R + B, 2R) slots of Hq * (D + 2) floats, R = 4 * CUs /
+ * head blocks flat ranges.  0 when bc_auto_splits, given the table's
+ * capacity (max_pages * 16 tokens), keeps the shape unsplit: a batch below
+ * R with a table under 512 tokens, one of at most 768 tokens whose
+ * (sequence, head block) workgroups fit the CUs, or one of at most 1024
+ * tokens whose workgroups fill half the CUs or more.  Such calls run
+ * unsplit, with no merge, whatever workspace is passed. */
 size_t bc_packed_decode_workspace_size(bc_shape shape);
 
 /* bc_packed_decode with the batch's pages spread over equal ranges of the
- * concatenated sequences, one workgroup per CU, and an FP32 merge of the
+ * concatenated sequences, one wave of workgroups (four waves per CU), and
+ * an FP32 merge of the
  * sequences a range boundary cuts.  The workgroup count and the workspace
  * size depend on the shape and the device's CU count only; the kernels find
  * the ranges from the lengths on the device, so no lengths are read on the

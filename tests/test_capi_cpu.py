@@ -198,8 +198,8 @@ def test_noalloc_rejects_before_launch():
     bad = capi.Shape(0, 32, 8, 128, 256, 20000)
     assert lib.bc_packed_decode_noalloc(bad, FAKE, FAKE, FAKE, FAKE, FAKE, *strides, 0.1,
                                         None) == INVALID
-    # 200 sequences of 128 query heads split, and their partials (30 MB)
-    # exceed the 16 MiB scratch
+    # 200 sequences of 128 query heads split, and their partials (two slots
+    # per range of 128: 17.0 MB) exceed the 16 MiB scratch
     big = capi.Shape(200, 128, 8, 128, 256, 20000)
     assert lib.bc_packed_decode_workspace_size(big) > capi.BC_STATIC_SCRATCH_BYTES
     assert lib.bc_packed_decode_noalloc(big, FAKE, FAKE, FAKE, FAKE, FAKE, *strides, 0.1,
@@ -207,16 +207,20 @@ def test_noalloc_rejects_before_launch():
 
 
 def test_auto_splits_policy():
-    """Split decode runs (splits - 1) * batch + 1 flat page ranges, rounded
-    down to whole waves of one workgroup per CU, each range served by
-    ceil(kv head blocks / 4) four-wave workgroups; the heuristic picks the
-    fewest splits that fill a wave, two splits for batches of one to two waves,
-    and keeps short contexts and larger batches unsplit."""
+    """Split decode runs min((splits - 1) * batch + 1, R) flat page ranges,
+    R = 4 * CUs / head blocks (one wave of workgroups at four waves per CU).
+    Batches of R or more take two splits at any context length; smaller
+    ones keep contexts below 512 tokens whole, stay whole while their
+    (sequence, head block) workgroups fit the CUs at up to 768 tokens, and
+    otherwise take the fewest splits whose ranges fill the wave."""
     lib = capi.load()
     assert lib.bc_auto_splits(_shape(batch=1), 63, 256) == 1  # tiny contexts stay whole
-    # below 512 tokens nothing splits, whatever the batch (src/paged_gqa.cu:135)
-    for batch in (1, 64, 512):
+    # below 512 tokens small batches stay whole (src/paged_gqa.cu:135) ...
+    for batch in (1, 64, 127):
         assert lib.bc_auto_splits(_shape(batch=batch), 511, 256) == 1
+    # ... and batches of a wave of ranges or more split at any length
+    for batch in (128, 512, 4096):
+        assert lib.bc_auto_splits(_shape(batch=batch), 16, 256) == 2
     # short contexts whose (sequence, head block) workgroups fit the CUs run
     # unsplit: eight waves share each sequence's pages, no merge kernel
     assert lib.bc_auto_splits(_shape(batch=1), 512, 256) == 1
@@ -227,7 +231,7 @@ def test_auto_splits_policy():
     assert lib.bc_auto_splits(_shape(batch=32), 1024, 256) == 1
     assert lib.bc_auto_splits(_shape(batch=33), 1024, 256) > 1
     assert lib.bc_auto_splits(_shape(batch=1), 1025, 256) > 1
-    ranges = 256 // 2  # 8 KV heads: two four-wave workgroups per range
+    ranges = 4 * 256 // 8  # 8 KV heads of 4 query heads: 8 head blocks
     for batch in (1, 2, 4, 16, 64, 100, 127):
         s = lib.bc_auto_splits(_shape(batch=batch), 32768, 256)
         assert 1 <= s <= capi.BC_MAX_SPLITS
@@ -236,10 +240,19 @@ def test_auto_splits_policy():
     assert lib.bc_auto_splits(_shape(batch=1), 32768, 256) == 128
     assert lib.bc_auto_splits(_shape(batch=4), 32768, 256) == 33
     assert lib.bc_auto_splits(_shape(batch=64), 4096, 256) == 3
-    for batch, splits in ((128, 2), (200, 2), (256, 2), (257, 1), (512, 1)):
-        assert lib.bc_auto_splits(_shape(batch=batch), 4096, 256) == splits, batch
-    # sixteen KV heads: four workgroups per range
+    for batch in (128, 200, 256, 257, 512, 1024):
+        assert lib.bc_auto_splits(_shape(batch=batch), 4096, 256) == 2, batch
+    # sixteen KV heads: 16 head blocks, 64 ranges
     assert lib.bc_auto_splits(_shape(batch=1, query_heads=16, kv_heads=16), 4096, 256) == 64
+    # one KV head of 8 query heads: one head block, 1024 ranges
+    one = dict(query_heads=8, kv_heads=1)
+    assert lib.bc_auto_splits(_shape(batch=1, **one), 32768, 256) == capi.BC_MAX_SPLITS
+    assert lib.bc_auto_splits(_shape(batch=8, **one), 32768, 256) == 129
+    assert lib.bc_auto_splits(_shape(batch=600, **one), 4096, 256) == 3
+    assert lib.bc_auto_splits(_shape(batch=1024, **one), 4096, 256) == 2
+    # 32 query heads on one KV head: two head blocks, 512 ranges
+    assert lib.bc_auto_splits(_shape(batch=512, query_heads=32, kv_heads=1), 100, 256) == 2
+    assert lib.bc_auto_splits(_shape(batch=511, query_heads=32, kv_heads=1), 100, 256) == 1
 
 
 def test_workspace_sizes():
@@ -254,10 +267,19 @@ def test_workspace_sizes():
     assert lib.bc_packed_decode_workspace_size(capi.Shape(4, 32, 8, 128, 49, 64)) > 0
     assert lib.bc_packed_decode_workspace_size(capi.Shape(32, 32, 8, 128, 64, 64)) == 0
     assert lib.bc_packed_decode_workspace_size(capi.Shape(32, 32, 8, 128, 65, 64)) > 0
-    # Tables below 512 tokens never split; from 512 on, batches whose
-    # workgroups outnumber the CUs do.
+    # Tables below 512 tokens split only for batches of a wave of ranges (128
+    # at 32/8 heads) or more; from 512 on, batches whose workgroups
+    # outnumber the CUs split too.
     assert lib.bc_packed_decode_workspace_size(capi.Shape(64, 32, 8, 128, 8, 64)) == 0
+    assert lib.bc_packed_decode_workspace_size(capi.Shape(128, 32, 8, 128, 8, 64)) > 0
     assert lib.bc_packed_decode_workspace_size(capi.Shape(64, 32, 8, 128, 32, 64)) > 0
+    # Partial slots per head: ranges + batch (C5: 128 + 64), or two per range
+    # once the batch outnumbers the ranges, whatever the batch.
+    row = 32 * (128 + 2) * 4  # one slot of every head: acc and (max, sum)
+    assert lib.bc_packed_decode_workspace_size(c5) == (128 + 64) * row
+    for batch in (129, 1024, 65536):
+        big = capi.Shape(batch, 32, 8, 128, 64, 70000)
+        assert lib.bc_packed_decode_workspace_size(big) == 2 * 128 * row, batch
     assert lib.bc_packed_decode_workspace_size(capi.Shape(4, 32, 8, 96, 80, 64)) == 0
     c3 = capi.Shape(8, 32, 8, 128, 129, 160)
     assert lib.bc_tree_verify_workspace_size(c3, 7) > 0

@@ -131,6 +131,23 @@ def test_unsplit_ragged_batches(batch, oracle):
     G.gate(G.decode(q, k, v, pages, lengths, 5), expected, 3e-4, f"B={batch} splits=5")
 
 
+def test_large_batch_short_contexts_split(oracle):
+    """A batch of a wave of flat ranges or more (128 at 32/8 heads) takes two
+    splits at contexts below 512 tokens too, so one wave of ranges streams
+    many sequences each; ragged lengths with empty sequences.  One split and
+    five splits (ranges capped at one wave) give the same result."""
+    rng = np.random.default_rng(300)
+    lens = rng.integers(0, 401, size=300)
+    lens[::11] = 0
+    q, k, v, pages, lengths = oracle_np.paged_fixture(rng, 300, 32, 8, 128, lens)
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    shape = capi.Shape(300, 32, 8, 128, pages.shape[1], k.shape[0])
+    assert G.lib().bc_auto_splits(shape, int(lens.max()), cus) == 2
+    expected = oracle.decode(q, k, v, pages, lengths, threads=16)
+    for splits in (2, 1, 5):
+        G.gate(G.decode(q, k, v, pages, lengths, splits), expected, 3e-4, f"splits={splits}")
+
+
 @pytest.mark.parametrize("out_shift,scratch_shift", [(4, 0), (0, 4), (8, 12)])
 def test_element_aligned_output_and_scratch(out_shift, scratch_shift, oracle):
     """The reference takes any `float*` for the output and the split

@@ -158,8 +158,7 @@ def test_long_sequences_many_partials(lens, oracle):
 
 def test_large_batch_takes_split_path(oracle):
     """128 sequences (one wave of flat ranges at 8 KV heads) run split with a
-    workspace; ragged lengths include empty sequences.  The table holds more
-    than 512 tokens: shorter tables never split (src/paged_gqa.cu:135)."""
+    workspace; ragged lengths include empty sequences."""
     torch.manual_seed(128)
     rng = np.random.default_rng(128)
     B, hq, hkv, d = 128, 32, 8, 128
@@ -186,6 +185,67 @@ def test_large_batch_takes_split_path(oracle):
         out = G.packed(q, cache, strides, hkv, NB, pages, lengths, scale, workspace=ws)
         err = np.abs(out.astype(np.float32) - exp32)
         assert np.all(err <= G.f16_tolerance(exp32, 2e-3)), f"ws={ws} max err {err.max():.3e}"
+
+
+def _packed_fixture(rng, lens, hq, hkv, d):
+    lens = np.asarray(lens, dtype=np.int32)
+    B = len(lens)
+    maxp = max(1, -(-int(lens.max()) // 16))
+    NB = sum(-(-int(n) // 16) for n in lens) + 8
+    cache = torch.randn((NB, 2, 16, hkv, d), device="cuda", dtype=torch.float16)
+    perm = rng.permutation(NB).astype(np.int32)
+    pages = np.full((B, maxp), -1, dtype=np.int32)
+    cur = 0
+    for i, n in enumerate(lens):
+        c = -(-int(n) // 16)
+        pages[i, :c] = perm[cur:cur + c]
+        cur += c
+    q = rng.standard_normal((B, hq, d)).astype(np.float16)
+    strides = (cache.stride(0), cache.stride(3), cache.stride(2), cache.stride(1))
+    return q, cache, strides, NB, pages, lens
+
+
+PAIR_CASES = {
+    # 200 sequences of 3 pages over 128 ranges of 5 pages: ranges start on a
+    # sequence's first page (its partial in slot 2r) and inside one (2r + 1)
+    "3-page-sequences": (32, 8, 128, lambda rng: np.full(200, 48)),
+    "ragged-with-empties": (32, 8, 128, lambda rng: np.where(np.arange(300) % 7 == 0, 0,
+                                                             rng.integers(1, 601, size=300))),
+    # one head block: 1024 ranges; two head blocks: 512 ranges
+    "one-kv-head": (8, 1, 64, lambda rng: rng.integers(0, 41, size=1100)),
+    "two-head-blocks": (32, 1, 128, lambda rng: rng.integers(1, 101, size=600)),
+}
+
+
+@pytest.mark.parametrize("case", list(PAIR_CASES))
+def test_batches_above_the_ranges_use_pair_slots(case, oracle):
+    """Batches of more sequences than flat ranges (4 * CUs / head blocks)
+    split at any context length, with two partial slots per range: a
+    workspace of 2 * ranges slots whatever the batch.  The workspace call
+    and the reference-signature call (its scratch a slot of the library's
+    pool, where the workspace fits one) give the same bits, within the
+    packed tolerance of the oracle."""
+    hq, hkv, d, make = PAIR_CASES[case]
+    rng = np.random.default_rng(len(case))
+    torch.manual_seed(len(case))
+    q, cache, strides, NB, pages, lens = _packed_fixture(rng, make(rng), hq, hkv, d)
+    B = len(lens)
+    zdim = hkv * -(-(hq // hkv) // 16)
+    ranges = 4 * torch.cuda.get_device_properties(0).multi_processor_count // zdim
+    assert B > ranges
+    need = G.lib().bc_packed_decode_workspace_size(capi.Shape(B, hq, hkv, d, pages.shape[1], NB))
+    assert need == 2 * ranges * hq * (d + 2) * 4, need
+    scale = 1 / math.sqrt(d)
+    exp32, _ = oracle.packed_decode(q, cache.cpu().numpy(), pages, lens, strides, hkv, scale,
+                                    threads=16)
+    outs = [G.packed(q, cache, strides, hkv, NB, pages, lens, scale, workspace=ws)
+            for ws in (True, False)]
+    for ws, out in zip((True, False), outs):
+        err = np.abs(out.astype(np.float32) - exp32)
+        assert np.all(err <= G.f16_tolerance(exp32, 2e-3)), f"ws={ws} max err {err.max():.3e}"
+    if need <= 8 << 20:  # fits a pool slot (BC_SCRATCH_SLOT_BYTES): the same split
+        assert np.array_equal(outs[0].view(np.uint16), outs[1].view(np.uint16))
+    assert np.all(exp32[lens == 0] == 0) and np.all(outs[0][lens == 0] == 0)
 
 
 def test_misaligned_workspace_is_ignored():

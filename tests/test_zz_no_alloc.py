@@ -84,6 +84,31 @@ def test_noalloc_matches_workspace_entry_point_twice():
         assert np.all(np.abs(got.astype(np.float32) - exp32) <= tol), f"batch {batch}"
 
 
+def test_noalloc_large_batches_use_pair_slots():
+    """Batches above the 128 flat ranges (32/8 heads) split with two partial
+    slots per range, 4.3 MB of the static array whatever the batch: 600
+    short sequences, then 200 longer ones, each bit-identical to the
+    workspace entry point and within tolerance of the oracle."""
+    rng = np.random.default_rng(57)
+    pool, hkv, d = 30000, 8, 128
+    cache = torch.randn((pool, 2, 16, hkv, d), device="cuda", dtype=torch.float16)
+    strides = (cache.stride(0), cache.stride(3), cache.stride(2), cache.stride(1))
+    scale = 1 / math.sqrt(d)
+    host_cache = cache.cpu().numpy()
+    for batch, lo, hi in ((600, 0, 300), (200, 100, 1500)):
+        q, pages, lens = _case(rng, batch, pool, lo=lo, hi=hi)
+        shape = capi.Shape(batch, 32, hkv, d, pages.shape[1], pool)
+        need = G.lib().bc_packed_decode_workspace_size(shape)
+        assert 0 < need <= capi.BC_STATIC_SCRATCH_BYTES, need
+        got = _run("noalloc", shape, q, cache, pages, lens, strides, scale)
+        ref = _run("ws", shape, q, cache, pages, lens, strides, scale)
+        assert np.array_equal(got.view(np.uint16), ref.view(np.uint16)), f"batch {batch}"
+        exp32, _ = oracle_c.packed_decode(q, host_cache, pages, lens, strides, hkv, scale,
+                                          threads=16)
+        tol = G.f16_tolerance(exp32, 2e-3)
+        assert np.all(np.abs(got.astype(np.float32) - exp32) <= tol), f"batch {batch}"
+
+
 def test_noalloc_unsplit_shape_and_oversize_rejection():
     """A short table runs unsplit (no scratch); an oversize shape returns
     hipErrorOutOfMemory and leaves the output untouched."""
