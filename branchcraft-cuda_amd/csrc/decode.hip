@@ -69,6 +69,9 @@ struct AttnParams {
   void* out;              // [B, Hq, D], float or _Float16
   float* part_acc;        // partials [slot][Hq][D] (slot: see pair_slots)
   float* part_ml;         // partials [slot][Hq][2]: (max in log2 units, sum)
+  int* range_meta;        // null, or [nwg]: 2 * (range's first sequence) + 1
+                          // if the range starts inside it (2 * batch for an
+                          // empty range), read by the merge kernel
   long long page_stride;  // elements between physical pages
   long long head_stride;  // elements between KV heads
   long long slot_stride;  // elements between page slots
@@ -91,7 +94,7 @@ struct AttnParams {
 // trip before the kernel's first memory access.
 __device__ __forceinline__ void pin_params(const AttnParams& P) {
   asm volatile("" ::"s"(P.q), "s"(P.kbase), "s"(P.vbase), "s"(P.pages), "s"(P.lengths),
-               "s"(P.out), "s"(P.part_acc), "s"(P.part_ml), "s"(P.page_stride),
+               "s"(P.out), "s"(P.part_acc), "s"(P.part_ml), "s"(P.range_meta), "s"(P.page_stride),
                "s"(P.head_stride), "s"(P.slot_stride), "s"(P.batch), "s"(P.hq), "s"(P.hkv),
                "s"(P.group), "s"(P.nblk), "s"(P.max_pages), "s"(P.phys_pages), "s"(P.zdim),
                "s"(P.waves), "s"(P.scale_log2), "s"(P.nwg), "s"(P.pair_slots));
@@ -122,14 +125,24 @@ __device__ __forceinline__ int pages_of(int len) {
 // Flat mode: workgroup rid's share of the batch's pages, `count` pages of
 // the concatenated sequences from local page `plocal` of sequence b, whose
 // length is len.  Lane i keeps sequence i's length in a register, so a batch
-// of up to 64 sequences costs one round of loads before the first page id
-// (larger batches load the lengths again for the search).
+// of up to 64 sequences costs one round of loads before the first page id.
+// Larger batches load the other lengths eight chunks of 64 per round (the
+// addresses clamped into the batch, so the loads need no branch): one round
+// for the page total per 512 sequences, and as many for the search up to
+// the chunk that holds the range's first page.
 __device__ void flat_range(const AttnParams& P, int lane, int rid, int& b, int& plocal,
                            int& count, int& len) {
+  constexpr int U = 8;  // chunks of 64 lengths per round of loads
   const int len0 = lane < P.batch ? seq_len(P, lane) : 0;
-  int total = wave_sum_i(pages_of(len0));
-  for (int base = 64; base < P.batch; base += 64)
-    total += wave_sum_i(base + lane < P.batch ? seq_pages(P, base + lane) : 0);
+  int mine = pages_of(len0);  // this lane's sequences lane, lane + 64, ...
+  for (int base = 64; base < P.batch; base += 64 * U) {
+    int l[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) l[u] = seq_len(P, min(base + 64 * u + lane, P.batch - 1));
+#pragma unroll
+    for (int u = 0; u < U; ++u) mine += base + 64 * u + lane < P.batch ? pages_of(l[u]) : 0;
+  }
+  const int total = wave_sum_i(mine);
   const int per = (total + P.nwg - 1) / P.nwg;
   const int f0 = rid * per;
   count = min(total, f0 + per) - f0;
@@ -137,21 +150,32 @@ __device__ void flat_range(const AttnParams& P, int lane, int rid, int& b, int& 
   plocal = 0;
   len = 0;
   if (count <= 0) return;
-  int run = 0;  // pages before sequence `base`
-  for (int base = 0; base < P.batch; base += 64) {
-    const int l = base == 0 ? len0 : (base + lane < P.batch ? seq_len(P, base + lane) : 0);
+  // The chunk of 64 sequences whose pages reach past f0 holds the range's
+  // first sequence: the first lane whose inclusive page count exceeds f0.
+  int run = 0;  // pages before the chunk
+  auto find = [&](int base, int l) -> bool {
     const int n = pages_of(l);
     const int inc = wave_incl_scan_i(n, lane);
     const int tot = __builtin_amdgcn_readlane(inc, 63);
-    if (run + tot > f0) {
-      const unsigned long long hit = __builtin_amdgcn_ballot_w64(run + inc > f0);
-      const int first = __builtin_ffsll((long long)hit) - 1;
-      b = base + first;
-      plocal = f0 - run - __builtin_amdgcn_readlane(inc - n, first);
-      len = __builtin_amdgcn_readlane(l, first);
-      return;
+    if (run + tot <= f0) {
+      run += tot;
+      return false;
     }
-    run += tot;
+    const unsigned long long hit = __builtin_amdgcn_ballot_w64(run + inc > f0);
+    const int first = __builtin_ffsll((long long)hit) - 1;
+    b = base + first;
+    plocal = f0 - run - __builtin_amdgcn_readlane(inc - n, first);
+    len = __builtin_amdgcn_readlane(l, first);
+    return true;
+  };
+  if (find(0, len0)) return;
+  for (int base = 64; base < P.batch; base += 64 * U) {
+    int l[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) l[u] = seq_len(P, min(base + 64 * u + lane, P.batch - 1));
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (find(base + 64 * u, base + 64 * u + lane < P.batch ? l[u] : 0)) return;
   }
 }
 
@@ -264,6 +288,8 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == kMaxWaves ? 3 : 2) void paged_
     count = (wave + 1) * np / WAVES - plocal;  // may be 0 (an empty slice)
   } else {
     flat_range(P, lane, rid, pb, plocal, count, plen);
+    if (P.range_meta && z == 0 && lane == 0)
+      P.range_meta[rid] = count > 0 ? 2 * pb + (plocal > 0 ? 1 : 0) : 2 * P.batch;
     if (count <= 0) return;
   }
   int ppages = pages_of(plen);
@@ -554,15 +580,53 @@ __global__ __launch_bounds__(256) void merge_kernel(AttnParams P) {
   // RW = 4 the whole workgroup leaves together.
   if (rowi >= P.batch * P.hq) return;
   const int b = rowi / P.hq, h = rowi % P.hq;
-  // One round of length loads: the batch's page total (as flat_range),
-  // the pages before sequence b and b's own page count.
-  int total = 0, before = 0, np = 0;
-  for (int base = 0; base < P.batch; base += 64) {
-    const int i = base + lane;
-    const int n = i < P.batch ? seq_pages(P, i) : 0;
-    total += wave_sum_i(n);
-    before += wave_sum_i(i < b ? n : 0);
-    if (b >= base && b < base + 64) np = __builtin_amdgcn_readlane(n, b - base);
+  // The ranges w0..w1 whose pages include sequence b's, and whether b is
+  // range w0's first sequence (w0_off = 0) or a later one (w0_off = 1).
+  int np, w0, w1, w0_off;
+  if (P.range_meta) {
+    // One round: b's length and the ranges' records.  The ranges whose
+    // first sequence is b are r1..r2; b began in range r1 - 1 if r1 starts
+    // inside it, else in r1.
+    np = seq_pages(P, b);
+    constexpr int U = 8;
+    int r1 = -1, r2 = -1, inside = 0;
+    for (int base = 0; base < P.nwg; base += 64 * U) {
+      int mv[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) mv[u] = P.range_meta[min(base + 64 * u + lane, P.nwg - 1)];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int r = base + 64 * u + lane;
+        const unsigned long long hit = __builtin_amdgcn_ballot_w64(r < P.nwg && mv[u] >> 1 == b);
+        if (hit) {
+          const int lo = __builtin_ffsll((long long)hit) - 1;
+          if (r1 < 0) {
+            r1 = base + 64 * u + lo;
+            inside = __builtin_amdgcn_readlane(mv[u], lo) & 1;
+          }
+          r2 = base + 64 * u + 63 - __builtin_clzll(hit);
+        }
+      }
+    }
+    w0 = r1 < 0 ? 0 : r1 - inside;
+    w1 = r1 < 0 ? 0 : r2;  // no range starts in b: b lies inside one range
+    w0_off = inside;
+  } else {
+    // Lengths of the whole batch, 64 per round: the page total (as
+    // flat_range), the pages before sequence b and b's own page count.
+    int total = 0, before = 0;
+    np = 0;
+    for (int base = 0; base < P.batch; base += 64) {
+      const int i = base + lane;
+      const int n = i < P.batch ? seq_pages(P, i) : 0;
+      total += wave_sum_i(n);
+      before += wave_sum_i(i < b ? n : 0);
+      if (b >= base && b < base + 64) np = __builtin_amdgcn_readlane(n, b - base);
+    }
+    const int per = max(1, (total + P.nwg - 1) / P.nwg);
+    w0 = before / per;
+    w1 = np > 0 ? (before + np - 1) / per : w0;
+    w0_off = w0 * per < before ? 1 : 0;
   }
   if (np == 0) {
     if (sub == 0) {
@@ -571,13 +635,11 @@ __global__ __launch_bounds__(256) void merge_kernel(AttnParams P) {
     }
     return;
   }
-  const int per = (total + P.nwg - 1) / P.nwg;
-  const int w0 = before / per, w1 = (before + np - 1) / per;
   if (w0 == w1) return;  // the sequence ended inside one range: written directly
   // Range w's partial slot (AttnParams::pair_slots).  With pair slots, b is
   // the first sequence of every range w0 < w <= w1 (they start on its
   // pages), and of range w0 only if w0 starts on b's first page.
-  const int w0_off = P.pair_slots && w0 * per < before ? 1 : 0;
+  if (!P.pair_slots) w0_off = 0;
   auto slot_of = [&](int w) { return P.pair_slots ? 2 * w + (w == w0 ? w0_off : 0) : w + b; };
   // This wave's partials: [r0, r1] (empty when r1 < r0).
   const int nparts = w1 - w0 + 1;
@@ -758,10 +820,12 @@ size_t packed_slots(const bc_shape& s, int nwg) {
   return s.batch > nwg ? 2 * (size_t)nwg : (size_t)nwg + s.batch;
 }
 
+// Workspace: partial accumulators (256-byte aligned), then their (max, sum)
+// pairs, then one record per range for the merge kernel.
 size_t packed_workspace(const bc_shape& s, int nwg) {
   const size_t slots = packed_slots(s, nwg);
   const size_t acc = (slots * s.query_heads * s.dim * sizeof(float) + 255) & ~(size_t)255;
-  return acc + slots * s.query_heads * 2 * sizeof(float);
+  return acc + slots * s.query_heads * 2 * sizeof(float) + (size_t)nwg * sizeof(int);
 }
 
 }  // namespace
@@ -795,6 +859,15 @@ extern "C" int bc_decode(bc_shape s, bc_inputs in, bc_scratch scratch,
   P.nwg = splits == 1 ? 0
                       : flat_workgroups(s.batch, (long long)splits * s.batch,
                                         flat_ranges(s, device_cus()));
+  // The range records go to the (max, sum) scratch past the slots in use
+  // where it has room for them; otherwise the merge kernel finds the ranges
+  // from the lengths.
+  if (P.nwg > 0) {
+    const long long used = (long long)P.nwg + s.batch - 1;
+    const long long spare = ((long long)splits * s.batch - used) * s.query_heads * 2;
+    if (spare >= P.nwg)
+      P.range_meta = reinterpret_cast<int*>(scratch.partial_ml + used * s.query_heads * 2);
+  }
   return launch<float>(P, s.dim, reinterpret_cast<hipStream_t>(stream));
 }
 
@@ -892,6 +965,7 @@ static int packed_common(bc_shape s, const bc_half* q, const bc_half* kv,
         (slots * s.query_heads * s.dim * sizeof(float) + 255) & ~(size_t)255;
     P.part_acc = static_cast<float*>(ws);
     P.part_ml = reinterpret_cast<float*>(static_cast<char*>(ws) + acc_bytes);
+    P.range_meta = reinterpret_cast<int*>(P.part_ml + slots * s.query_heads * 2);
   }
   return launch<_Float16>(P, s.dim, reinterpret_cast<hipStream_t>(stream));
 }

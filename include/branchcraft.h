@@ -239,8 +239,8 @@ int bc_packed_decode(bc_shape shape, const bc_half* q, const bc_half* packed_kv,
                      long long kv_stride, float scale, bc_stream_t stream);
 
 /* Bytes of workspace bc_packed_decode_ws needs for this shape: FP32
- * partials of min(R + B, 2R) slots of Hq * (D + 2) floats, R = 4 * CUs /
- * head blocks flat ranges.  0 when bc_auto_splits, given the table's
+ * partials of min(R + B, 2R) slots of Hq * (D + 2) floats and one int per
+ * range, R = 4 * CUs / head blocks flat ranges.  0 when bc_auto_splits, given the table's
  * capacity (max_pages * 16 tokens), keeps the shape unsplit: a batch below
  * R with a table under 512 tokens, one of at most 768 tokens whose
  * (sequence, head block) workgroups fit the CUs, or one of at most 1024

@@ -234,7 +234,7 @@ def test_batches_above_the_ranges_use_pair_slots(case, oracle):
     ranges = 4 * torch.cuda.get_device_properties(0).multi_processor_count // zdim
     assert B > ranges
     need = G.lib().bc_packed_decode_workspace_size(capi.Shape(B, hq, hkv, d, pages.shape[1], NB))
-    assert need == 2 * ranges * hq * (d + 2) * 4, need
+    assert need == 2 * ranges * hq * (d + 2) * 4 + ranges * 4, need
     scale = 1 / math.sqrt(d)
     exp32, _ = oracle.packed_decode(q, cache.cpu().numpy(), pages, lens, strides, hkv, scale,
                                     threads=16)
