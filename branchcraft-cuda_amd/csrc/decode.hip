@@ -122,6 +122,21 @@ __device__ __forceinline__ int pages_of(int len) {
   return (len + BC_PAGE_SIZE - 1) / BC_PAGE_SIZE;
 }
 
+// Lengths of 64 consecutive sequences, lane i holding sequence base + i's
+// (clamped), so that a cursor stepping into the next sequence reads its
+// length from a register instead of waiting for a load queued behind the
+// pages in flight.  A step past the window loads the next one.
+struct LenWindow {
+  int base, len;
+  __device__ __forceinline__ int at(const AttnParams& P, int lane, int i) {
+    if (i - base >= 64) {
+      base = i;
+      len = seq_len(P, min(i + lane, P.batch - 1));
+    }
+    return __builtin_amdgcn_readlane(len, __builtin_amdgcn_readfirstlane(i - base));
+  }
+};
+
 // Flat mode: workgroup rid's share of the batch's pages, `count` pages of
 // the concatenated sequences from local page `plocal` of sequence b, whose
 // length is len.  Lane i keeps sequence i's length in a register, so a batch
@@ -131,7 +146,7 @@ __device__ __forceinline__ int pages_of(int len) {
 // for the page total per 512 sequences, and as many for the search up to
 // the chunk that holds the range's first page.
 __device__ void flat_range(const AttnParams& P, int lane, int rid, int& b, int& plocal,
-                           int& count, int& len) {
+                           int& count, int& len, LenWindow& win) {
   constexpr int U = 8;  // chunks of 64 lengths per round of loads
   const int len0 = lane < P.batch ? seq_len(P, lane) : 0;
   int mine = pages_of(len0);  // this lane's sequences lane, lane + 64, ...
@@ -149,6 +164,7 @@ __device__ void flat_range(const AttnParams& P, int lane, int rid, int& b, int& 
   b = 0;
   plocal = 0;
   len = 0;
+  win = LenWindow{0, len0};
   if (count <= 0) return;
   // The chunk of 64 sequences whose pages reach past f0 holds the range's
   // first sequence: the first lane whose inclusive page count exceeds f0.
@@ -166,6 +182,7 @@ __device__ void flat_range(const AttnParams& P, int lane, int rid, int& b, int& 
     b = base + first;
     plocal = f0 - run - __builtin_amdgcn_readlane(inc - n, first);
     len = __builtin_amdgcn_readlane(l, first);
+    win = LenWindow{base, l};
     return true;
   };
   if (find(0, len0)) return;
@@ -281,13 +298,15 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == kMaxWaves ? 3 : 2) void paged_
   // This workgroup's pages: sequence pb from local page `plocal`, `count`
   // pages in all (crossing into later sequences in flat mode).
   int pb, plocal, count, plen;
+  LenWindow iwin{0, 0}, cwin{0, 0};  // lengths for the issue and compute cursors
   if (sliced) {
     pb = seq_by_rank(P, lane, rid, plen);
     const int np = pages_of(plen);
     plocal = wave * np / WAVES;
     count = (wave + 1) * np / WAVES - plocal;  // may be 0 (an empty slice)
   } else {
-    flat_range(P, lane, rid, pb, plocal, count, plen);
+    flat_range(P, lane, rid, pb, plocal, count, plen, iwin);
+    cwin = iwin;
     if (P.range_meta && z == 0 && lane == 0)
       P.range_meta[rid] = count > 0 ? 2 * pb + (plocal > 0 ? 1 : 0) : 2 * P.batch;
     if (count <= 0) return;
@@ -368,7 +387,7 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == kMaxWaves ? 3 : 2) void paged_
     if (++ilocal == ipages && issued < count) {
       do {
         ++ib;
-        ipages = seq_pages(P, ib);
+        ipages = pages_of(iwin.at(P, lane, ib));
       } while (ipages == 0);
       ilocal = 0;
     }
@@ -453,9 +472,9 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == kMaxWaves ? 3 : 2) void paged_
       if (idx + 1 < count) {
         do {
           ++pb;
-          ppages = seq_pages(P, pb);
+          plen = cwin.at(P, lane, pb);
+          ppages = pages_of(plen);
         } while (ppages == 0);
-        plen = seq_len(P, pb);
         plocal = 0;
         seg0 = 0;
         load_q(pb);
