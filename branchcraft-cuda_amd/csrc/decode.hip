@@ -895,6 +895,12 @@ extern "C" int bc_auto_splits(bc_shape s, int max_length, int cu_count) {
   // split kSlices ways inside it and no merge kernel.  splits > 1 runs flat
   // page ranges, min((splits - 1) * batch + 1, R) of them, R = flat_ranges
   // (one wave of workgroups at four waves per CU).
+  //  - With one or two head blocks, batches whose (sequence, head block)
+  //    workgroups fill the CUs stay whole: eight waves per CU beat the
+  //    ranges' four there (same box, 1024 tokens: 8/1 heads, 512 sequences
+  //    30.5 against 35.5 us at three splits; 16/2 heads, 256 sequences 31.9
+  //    against 35.6 us; 1024 sequences of up to 400 tokens, where two
+  //    splits are 3 % faster, are the exception measured).
   //  - Batches of R sequences or more take two splits, so R ranges, whatever
   //    the context length: one wave of workgroups streaming many sequences
   //    each beats a launch of one workgroup per (sequence, head block) in
@@ -913,6 +919,8 @@ extern "C" int bc_auto_splits(bc_shape s, int max_length, int cu_count) {
   const int cus = cu_count > 0 ? cu_count : 256;
   const int ranges = flat_ranges(s, cus);
   if (ranges <= 1) return 1;
+  const long long wgs = (long long)s.batch * zdim_of(s);
+  if (zdim_of(s) <= 2 && wgs >= cus) return 1;
   if (s.batch >= ranges) return 2;
   if (max_length < 512) return 1;
   // Unsplit up to 768 tokens; up to 1024 only where the batch's workgroups
@@ -920,7 +928,6 @@ extern "C" int bc_auto_splits(bc_shape s, int max_length, int cu_count) {
   // one sequence 12.3 us unsplit against 9.7 us split, 8 sequences 14.4
   // against 12.7, 12 sequences 16.0 against 16.0, 16 sequences 17.0 against
   // 18.0, 32 sequences 23.5 against 24.9 at the best split count).
-  const long long wgs = (long long)s.batch * zdim_of(s);
   if (wgs <= cus && (max_length <= 768 || (max_length <= 1024 && 2 * wgs >= cus))) return 1;
   long long splits = ((long long)ranges + 2LL * s.batch - 2) / s.batch;
   if (splits > BC_MAX_SPLITS) splits = BC_MAX_SPLITS;

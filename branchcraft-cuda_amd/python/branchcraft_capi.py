@@ -20,6 +20,8 @@ BC_SUCCESS = 0
 BC_ERROR_INVALID_VALUE = 1
 BC_ERROR_OUT_OF_MEMORY = 2
 BC_STATIC_SCRATCH_BYTES = 16 << 20
+BC_SCRATCH_SLOTS = 4
+BC_SCRATCH_SLOT_BYTES = 18 << 20
 BC_PAGE_SIZE = 16
 BC_MAX_SPLITS = 256
 BC_MAX_TREE_NODES = 256

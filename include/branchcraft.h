@@ -12,8 +12,9 @@
  * State, per device: a cache of the CU count, and the split-scratch pool
  * that the entry points without a workspace argument (bc_packed_decode,
  * bc_tree_verify) borrow from -- BC_SCRATCH_SLOTS slots of
- * BC_SCRATCH_SLOT_BYTES in a static device array (32 MiB per GPU the
- * library runs on, held until the process ends).  A call on a stream takes
+ * BC_SCRATCH_SLOT_BYTES in a static device array (72 MiB per GPU the
+ * library runs on, held until the process ends; a slot holds the split
+ * workspace of every packed decode shape up to D = 128 on 256 CUs).  A call on a stream takes
  * the slot that stream used last (reused in stream order), else a free
  * slot, else the least recently used slot whose last use was recorded in
  * the slot's event, which the stream then waits for on the device
@@ -56,7 +57,7 @@ enum {
 /* The split-scratch pool of bc_packed_decode and bc_tree_verify: slots per
  * GPU and bytes per slot. */
 #define BC_SCRATCH_SLOTS 4
-#define BC_SCRATCH_SLOT_BYTES (8u << 20)
+#define BC_SCRATCH_SLOT_BYTES (18u << 20)
 
 /* Tokens per KV page (reference: kPageSize, include/branchcraft.hpp:8). */
 #define BC_PAGE_SIZE 16
@@ -125,9 +126,10 @@ int bc_decode(bc_shape shape, bc_inputs in, bc_scratch scratch, int splits,
               bc_stream_t stream);
 
 /* Split-count heuristic for bc_decode on a device with `cu_count` compute
- * units; returns a value in [1, BC_MAX_SPLITS]: 2 for batches of at least
- * one wave of flat ranges (4 * cu_count / head blocks: 128 sequences at 8
- * KV heads of 4 query heads on 256 CUs) at any length, else 1 for
+ * units; returns a value in [1, BC_MAX_SPLITS]: 1 with one or two head
+ * blocks once batch * head blocks >= cu_count; else 2 for batches of at
+ * least one wave of flat ranges (4 * cu_count / head blocks: 128 sequences
+ * at 8 KV heads of 4 query heads on 256 CUs) at any length; else 1 for
  * max_length < 512.
  * Replaces branchcraft::auto_splits, include/branchcraft.hpp:41
  * (src/paged_gqa.cu:134-142), retuned for 256-CU MI355X workgroups: unlike
@@ -241,10 +243,11 @@ int bc_packed_decode(bc_shape shape, const bc_half* q, const bc_half* packed_kv,
 /* Bytes of workspace bc_packed_decode_ws needs for this shape: FP32
  * partials of min(R + B, 2R) slots of Hq * (D + 2) floats and one int per
  * range, R = 4 * CUs / head blocks flat ranges.  0 when bc_auto_splits, given the table's
- * capacity (max_pages * 16 tokens), keeps the shape unsplit: a batch below
- * R with a table under 512 tokens, one of at most 768 tokens whose
- * (sequence, head block) workgroups fit the CUs, or one of at most 1024
- * tokens whose workgroups fill half the CUs or more.  Such calls run
+ * capacity (max_pages * 16 tokens), keeps the shape unsplit: one or two
+ * head blocks whose (sequence, head block) workgroups fill the CUs; a batch
+ * below R with a table under 512 tokens, one of at most 768 tokens whose
+ * workgroups fit the CUs, or one of at most 1024 tokens whose workgroups
+ * fill half the CUs or more.  Such calls run
  * unsplit, with no merge, whatever workspace is passed. */
 size_t bc_packed_decode_workspace_size(bc_shape shape);
 

@@ -206,6 +206,23 @@ def test_noalloc_rejects_before_launch():
                                         None) == capi.BC_ERROR_OUT_OF_MEMORY
 
 
+def test_packed_workspace_fits_a_pool_slot():
+    """Every packed decode workspace up to D = 128 on 256 CUs fits a slot of
+    the scratch pool, so the reference-signature call splits wherever the
+    workspace call does: 2R slots of Hq (D + 2) floats with R = 1024 / head
+    blocks and head blocks >= Hq / 16 stay within 128 * 256 * 130 * 4 bytes
+    plus the range records, whatever the batch and heads."""
+    lib = capi.load()
+    worst = 0
+    for hq, hkv in ((128, 1), (128, 8), (64, 1), (32, 1), (16, 1), (8, 1), (32, 8), (48, 3),
+                    (64, 64), (1, 1)):
+        for batch in (1, 64, 1000, 100000):
+            need = lib.bc_packed_decode_workspace_size(capi.Shape(batch, hq, hkv, 128, 4096, 10**6))
+            worst = max(worst, need)
+            assert need <= capi.BC_SCRATCH_SLOT_BYTES, (hq, hkv, batch, need)
+    assert worst >= 128 * 256 * 130 * 4  # the bound is reached
+
+
 def test_auto_splits_policy():
     """Split decode runs min((splits - 1) * batch + 1, R) flat page ranges,
     R = 4 * CUs / head blocks (one wave of workgroups at four waves per CU).
@@ -244,15 +261,21 @@ def test_auto_splits_policy():
         assert lib.bc_auto_splits(_shape(batch=batch), 4096, 256) == 2, batch
     # sixteen KV heads: 16 head blocks, 64 ranges
     assert lib.bc_auto_splits(_shape(batch=1, query_heads=16, kv_heads=16), 4096, 256) == 64
-    # one KV head of 8 query heads: one head block, 1024 ranges
+    # one KV head of 8 query heads: one head block, 1024 ranges; whole from
+    # 256 sequences on (their workgroups fill the CUs)
     one = dict(query_heads=8, kv_heads=1)
     assert lib.bc_auto_splits(_shape(batch=1, **one), 32768, 256) == capi.BC_MAX_SPLITS
     assert lib.bc_auto_splits(_shape(batch=8, **one), 32768, 256) == 129
-    assert lib.bc_auto_splits(_shape(batch=600, **one), 4096, 256) == 3
-    assert lib.bc_auto_splits(_shape(batch=1024, **one), 4096, 256) == 2
-    # 32 query heads on one KV head: two head blocks, 512 ranges
-    assert lib.bc_auto_splits(_shape(batch=512, query_heads=32, kv_heads=1), 100, 256) == 2
-    assert lib.bc_auto_splits(_shape(batch=511, query_heads=32, kv_heads=1), 100, 256) == 1
+    assert lib.bc_auto_splits(_shape(batch=255, **one), 4096, 256) == 6
+    for batch in (256, 600, 1024, 4096):
+        assert lib.bc_auto_splits(_shape(batch=batch, **one), 4096, 256) == 1, batch
+    # 32 query heads on one KV head: two head blocks, whole from 128 sequences
+    two = dict(query_heads=32, kv_heads=1)
+    assert lib.bc_auto_splits(_shape(batch=127, **two), 4096, 256) == 6
+    assert lib.bc_auto_splits(_shape(batch=128, **two), 4096, 256) == 1
+    # 32 query heads on 4 KV heads: four head blocks, 256 ranges
+    assert lib.bc_auto_splits(_shape(batch=256, query_heads=32, kv_heads=4), 100, 256) == 2
+    assert lib.bc_auto_splits(_shape(batch=255, query_heads=32, kv_heads=4), 100, 256) == 1
 
 
 def test_workspace_sizes():

@@ -211,9 +211,10 @@ PAIR_CASES = {
     "3-page-sequences": (32, 8, 128, lambda rng: np.full(200, 48)),
     "ragged-with-empties": (32, 8, 128, lambda rng: np.where(np.arange(300) % 7 == 0, 0,
                                                              rng.integers(1, 601, size=300))),
-    # one head block: 1024 ranges; two head blocks: 512 ranges
-    "one-kv-head": (8, 1, 64, lambda rng: rng.integers(0, 41, size=1100)),
-    "two-head-blocks": (32, 1, 128, lambda rng: rng.integers(1, 101, size=600)),
+    # three head blocks: 341 ranges; four: 256; 32 (no grouping): 32
+    "three-head-blocks": (48, 3, 64, lambda rng: rng.integers(0, 201, size=500)),
+    "four-head-blocks": (32, 4, 128, lambda rng: rng.integers(1, 301, size=400)),
+    "32-head-blocks": (32, 32, 64, lambda rng: rng.integers(0, 501, size=100)),
 }
 
 
@@ -243,7 +244,7 @@ def test_batches_above_the_ranges_use_pair_slots(case, oracle):
     for ws, out in zip((True, False), outs):
         err = np.abs(out.astype(np.float32) - exp32)
         assert np.all(err <= G.f16_tolerance(exp32, 2e-3)), f"ws={ws} max err {err.max():.3e}"
-    if need <= 8 << 20:  # fits a pool slot (BC_SCRATCH_SLOT_BYTES): the same split
+    if need <= capi.BC_SCRATCH_SLOT_BYTES:  # fits a pool slot: the same split
         assert np.array_equal(outs[0].view(np.uint16), outs[1].view(np.uint16))
     assert np.all(exp32[lens == 0] == 0) and np.all(outs[0][lens == 0] == 0)
 

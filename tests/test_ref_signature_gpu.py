@@ -107,7 +107,7 @@ def test_packed_reference_signature_equals_workspace_call(case):
     else:
         p = Packed(rng, 4, 16384, 32768, 8192)
     need = G.lib().bc_packed_decode_workspace_size(p.shape)
-    assert 0 < need <= 8 << 20
+    assert 0 < need <= capi.BC_SCRATCH_SLOT_BYTES
     a, b = p.out(), p.out()
     p.call(a, G.stream())
     p.call(b, G.stream(), ws=_ws(need))
@@ -121,7 +121,7 @@ def test_tree_reference_signature_equals_workspace_call(batch, prefix, oracle):
     rng = np.random.default_rng(batch * 7 + prefix)
     t = Tree(rng, batch, prefix)
     need = G.lib().bc_tree_verify_workspace_size(t.shape, t.nodes)
-    assert 0 < need <= 8 << 20
+    assert 0 < need <= capi.BC_SCRATCH_SLOT_BYTES
     a, b = t.out(), t.out()
     t.call(a, G.stream())
     t.call(b, G.stream(), ws=_ws(need))
