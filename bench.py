@@ -46,7 +46,7 @@ HBM_PEAK_GBS = 8000.0
 # HBM bytes per config-5 call measured with rocprofv3 counters: attention
 # FETCH 264,747.1 KiB x 2 + WRITE 3,021.5 KiB, merge FETCH 1,573.5 KiB x 2 +
 # WRITE 448.0 KiB (FETCH_SIZE reads half of a 512 MiB copy's bytes).
-C5_HBM_TRAFFIC_BYTES = (264747.1 * 2 + 3021.5 + 1573.5 * 2 + 448.0) * 1024
+C5_HBM_TRAFFIC_BYTES = (264758.3 * 2 + 3023.5 + 1598.0 * 2 + 448.0) * 1024
 MFMA_F16_PEAK_TFLOPS = 2500.0
 PAGE = 16
 
@@ -743,7 +743,7 @@ def main():
             "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": C5_HBM_TRAFFIC_BYTES,
             "traffic_source": "rocprofv3 FETCH_SIZE (x2) + WRITE_SIZE (x1) per call, scaled "
                               "by a 512 MiB copy; profiles/packed_decode_c5_hbm_traffic.md",
-            "kernel": ("paged_attn_kernel<128,_Float16,true,4> + merge_kernel<128,_Float16,1> "
+            "kernel": ("paged_attn_kernel<128,_Float16,true,4> + merge_kernel<128,_Float16,1,false,false> "
                        "(one bc_packed_decode_ws call; achieved = algorithmic bytes / "
                        "HIP-event time per call on the launch stream)"),
             "algorithmic_bytes_per_launch": c5.bytes,

@@ -345,8 +345,9 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == kMaxWaves ? 3 : 2) void paged_
                           acc[t][2] * inv, acc[t][3] * inv);
     } else {
       // A range cuts at most two sequences: its first (which started in an
-      // earlier range) and its last (which goes on in the next one).
-      const int slot = P.pair_slots ? 2 * rid + (pb != pb_first ? 1 : 0) : rid + pb;
+      // earlier range) and its last (which goes on in the next one).  Plain
+      // arithmetic: a select on pair_slots becomes a branch.
+      const int slot = rid + pb + P.pair_slots * (rid + (pb != pb_first) - pb);
       const size_t r = (size_t)slot * P.hq + h;
       float* pa = P.part_acc + r * D + 4 * g4;
 #pragma unroll
@@ -586,7 +587,7 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == kMaxWaves ? 3 : 2) void paged_
 // each wave combines a contiguous quarter of the row's partials and wave 0
 // merges the four states through LDS: rows of a few long sequences have
 // hundreds of partials, too many for one wave.
-template <int D, typename OutT, int RW>
+template <int D, typename OutT, int RW, bool PAIR, bool META>
 __global__ __launch_bounds__(256) void merge_kernel(AttnParams P) {
   pin_params(P);
   static_assert(RW == 1 || RW == 4, "one or four waves per row");
@@ -602,7 +603,7 @@ __global__ __launch_bounds__(256) void merge_kernel(AttnParams P) {
   // The ranges w0..w1 whose pages include sequence b's, and whether b is
   // range w0's first sequence (w0_off = 0) or a later one (w0_off = 1).
   int np, w0, w1, w0_off;
-  if (P.range_meta) {
+  if constexpr (META) {
     // One round: b's length and the ranges' records.  The ranges whose
     // first sequence is b are r1..r2; b began in range r1 - 1 if r1 starts
     // inside it, else in r1.
@@ -658,8 +659,9 @@ __global__ __launch_bounds__(256) void merge_kernel(AttnParams P) {
   // Range w's partial slot (AttnParams::pair_slots).  With pair slots, b is
   // the first sequence of every range w0 < w <= w1 (they start on its
   // pages), and of range w0 only if w0 starts on b's first page.
-  if (!P.pair_slots) w0_off = 0;
-  auto slot_of = [&](int w) { return P.pair_slots ? 2 * w + (w == w0 ? w0_off : 0) : w + b; };
+  // PAIR = pair_slots, a template argument: the slot arithmetic sits in the
+  // address of every partial load below, ahead of the row's memory round.
+  auto slot_of = [&](int w) { return PAIR ? 2 * w + w0_off * (w == w0) : w + b; };
   // This wave's partials: [r0, r1] (empty when r1 < r0).
   const int nparts = w1 - w0 + 1;
   const int r0 = w0 + sub * nparts / RW, r1 = w0 + (sub + 1) * nparts / RW - 1;
@@ -771,11 +773,20 @@ hipError_t launch_dim(const AttnParams& P, bool vec, hipStream_t st) {
   hipError_t err = hipGetLastError();
   if (err != hipSuccess || P.nwg == 0) return err;
   const unsigned rows = (unsigned)P.batch * P.hq;
-  // Four waves per row once the ranges outnumber the sequences 16 to 1.
+  // Four waves per row once the ranges outnumber the sequences 16 to 1
+  // (never with pair slots, which need more sequences than ranges).
+  // Range records come with more than 64 sequences (below, RW = 1).
+  const dim3 g1((rows + 3) / 4);
   if (P.nwg >= 16 * P.batch)
-    merge_kernel<D, OutT, 4><<<dim3(rows), 256, 0, st>>>(P);
+    merge_kernel<D, OutT, 4, false, false><<<dim3(rows), 256, 0, st>>>(P);
+  else if (P.range_meta && P.pair_slots)
+    merge_kernel<D, OutT, 1, true, true><<<g1, 256, 0, st>>>(P);
+  else if (P.range_meta)
+    merge_kernel<D, OutT, 1, false, true><<<g1, 256, 0, st>>>(P);
+  else if (P.pair_slots)
+    merge_kernel<D, OutT, 1, true, false><<<g1, 256, 0, st>>>(P);
   else
-    merge_kernel<D, OutT, 1><<<dim3((rows + 3) / 4), 256, 0, st>>>(P);
+    merge_kernel<D, OutT, 1, false, false><<<g1, 256, 0, st>>>(P);
   return hipGetLastError();
 }
 
@@ -878,10 +889,10 @@ extern "C" int bc_decode(bc_shape s, bc_inputs in, bc_scratch scratch,
   P.nwg = splits == 1 ? 0
                       : flat_workgroups(s.batch, (long long)splits * s.batch,
                                         flat_ranges(s, device_cus()));
-  // The range records go to the (max, sum) scratch past the slots in use
-  // where it has room for them; otherwise the merge kernel finds the ranges
-  // from the lengths.
-  if (P.nwg > 0) {
+  // Above 64 sequences the range records go to the (max, sum) scratch past
+  // the slots in use where it has room for them; otherwise the merge kernel
+  // finds the ranges from the lengths.
+  if (P.nwg > 0 && s.batch > 64) {
     const long long used = (long long)P.nwg + s.batch - 1;
     const long long spare = ((long long)splits * s.batch - used) * s.query_heads * 2;
     if (spare >= P.nwg)
@@ -991,7 +1002,9 @@ static int packed_common(bc_shape s, const bc_half* q, const bc_half* kv,
         (slots * s.query_heads * s.dim * sizeof(float) + 255) & ~(size_t)255;
     P.part_acc = static_cast<float*>(ws);
     P.part_ml = reinterpret_cast<float*>(static_cast<char*>(ws) + acc_bytes);
-    P.range_meta = reinterpret_cast<int*>(P.part_ml + slots * s.query_heads * 2);
+    // Up to 64 sequences the merge kernel reads every length in one round
+    // anyway; the range records pay from there on.
+    if (s.batch > 64) P.range_meta = reinterpret_cast<int*>(P.part_ml + slots * s.query_heads * 2);
   }
   return launch<_Float16>(P, s.dim, reinterpret_cast<hipStream_t>(stream));
 }

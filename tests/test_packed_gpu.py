@@ -215,6 +215,8 @@ PAIR_CASES = {
     "three-head-blocks": (48, 3, 64, lambda rng: rng.integers(0, 201, size=500)),
     "four-head-blocks": (32, 4, 128, lambda rng: rng.integers(1, 301, size=400)),
     "32-head-blocks": (32, 32, 64, lambda rng: rng.integers(0, 501, size=100)),
+    # at most 64 sequences: the merge finds the ranges from the lengths
+    "32-head-blocks-60": (32, 32, 64, lambda rng: rng.integers(0, 301, size=60)),
 }
 
 
