@@ -173,3 +173,66 @@ def test_random_packed_decode(seed, oracle):
         assert np.all(np.isfinite(out)), f"{what} workspace={ws} shift={sh}: non-finite output"
         assert np.all(err <= G.f16_tolerance(expected, 3e-4)), \
             f"{what} workspace={ws} shift={sh}: max err {err.max():.3e}"
+
+
+def _large_batch_case(seed):
+    """65 to 1500 sequences of short contexts (empty ones included): the
+    flat ranges of one wave then cover many sequences each, and the merge
+    finds its ranges from the range records; packed batches above the range
+    count use two partial slots per range."""
+    rng = np.random.default_rng(9000 + seed)
+    d = int(rng.choice([64, 128]))
+    hq, hkv = LAYOUTS[rng.integers(len(LAYOUTS))]
+    maxlen = int(rng.choice([16, 100, 400, 1200]))
+    batch = int(rng.integers(65, 1501))
+    # Bound the fixture (K and V elements) and the oracle's work.
+    while batch > 65 and (batch * maxlen * hkv * d > 1e8 or batch * hq * maxlen > 12e6):
+        batch = max(65, batch * 3 // 4)
+    lengths = rng.integers(0, maxlen + 1, size=batch).astype(np.int32)
+    lengths[rng.random(batch) < 0.1] = 0
+    lengths[rng.integers(batch)] = maxlen
+    q, k, v, pages, lengths = oracle_np.paged_fixture(rng, batch, hq, hkv, d, lengths,
+                                                      spare=int(rng.integers(1, 9)))
+    what = f"seed={seed} B={batch} H={hq}/{hkv} D={d} maxlen={maxlen}"
+    return (q, k, v, pages, lengths), rng, what
+
+
+@pytest.mark.parametrize("seed", _seeds(8))
+def test_random_large_batch_paged_decode(seed, oracle):
+    """bc_decode over a large batch at the auto split count, two splits and
+    a random count up to 9."""
+    (q, k, v, pages, lengths), rng, what = _large_batch_case(seed)
+    print(what, flush=True)
+    expected = oracle.decode(q, k, v, pages, lengths, threads=16)
+    b, hq, d = q.shape
+    auto = G.lib().bc_auto_splits(capi.Shape(b, hq, k.shape[2], d, pages.shape[1], k.shape[0]),
+                                  int(lengths.max()), 256)
+    for splits in sorted({int(auto), 2, int(rng.integers(3, 10))}):
+        out = G.decode(q, k, v, pages, lengths, splits)
+        G.gate(out, expected, 3e-4, f"{what} splits={splits}")
+
+
+@pytest.mark.parametrize("seed", _seeds(8))
+def test_random_large_batch_packed_decode(seed, oracle):
+    """bc_packed_decode_ws and bc_packed_decode ([P, 2, 16, Hkv, D] cache)
+    over a large batch: within tolerance of the oracle, and bit-identical to
+    each other, since every packed workspace fits a slot of the pool."""
+    (q, k, v, pages, lengths), rng, what = _large_batch_case(100 + seed)
+    print(what, flush=True)
+    P, _, hkv, d = k.shape
+    cache = torch.from_numpy(np.ascontiguousarray(np.stack([k, v], axis=1))).cuda()
+    strides = (cache.stride(0), cache.stride(3), cache.stride(2), cache.stride(1))
+    scale = 1 / math.sqrt(d)
+    expected, _ = oracle.packed_decode(q, cache.cpu().numpy(), pages, lengths, strides, hkv,
+                                       scale, threads=16)
+    need = G.lib().bc_packed_decode_workspace_size(
+        capi.Shape(q.shape[0], q.shape[1], hkv, d, pages.shape[1], P))
+    assert need <= capi.BC_SCRATCH_SLOT_BYTES, need
+    outs = [G.packed(q, cache, strides, hkv, P, pages, lengths, scale, workspace=ws)
+            for ws in (True, False)]
+    for ws, out in zip((True, False), outs):
+        err = np.abs(out.astype(np.float32) - expected)
+        assert np.all(np.isfinite(out)), f"{what} workspace={ws}: non-finite output"
+        assert np.all(err <= G.f16_tolerance(expected, 3e-4)), \
+            f"{what} workspace={ws}: max err {err.max():.3e}"
+    assert np.array_equal(outs[0].view(np.uint16), outs[1].view(np.uint16)), what
