@@ -11,10 +11,12 @@
 // head block (up to four) and walks an equal share of all the batch's
 // pages: workgroup w of W takes pages [w*T/W, (w+1)*T/W) of the
 // concatenated sequences, crossing sequence boundaries as it goes, so every
-// workgroup does the same work however ragged the lengths are.  A sequence
-// that ends inside one workgroup's range is written directly; the others
-// leave an FP32 partial (max, sum, acc) per workgroup and a merge kernel
-// combines them.  Unsplit decode: one workgroup per (sequence, head block)
+// workgroup does the same work however ragged the lengths are; W is at most
+// one wave of workgroups (four waves per CU).  A sequence that ends inside
+// one workgroup's range is written directly; the others leave an FP32
+// partial (max, sum, acc) per workgroup, and a merge kernel combines them,
+// finding a sequence's ranges from the lengths or, above 64 sequences, from
+// one record per range.  Unsplit decode: one workgroup per (sequence, head block)
 // whose eight waves take eighths of the sequence's pages and merge their
 // states through LDS.  Inside a wave, one 16-token page and the query heads
 // of one KV head (the GQA group, up to 16) form MFMA tiles:
