@@ -597,43 +597,61 @@ __global__ __launch_bounds__(256) void merge_kernel(AttnParams P) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int sub = wave % RW;  // this wave's share of the row's partials
-  const int rowi = blockIdx.x * (4 / RW) + wave / RW;
-  // Every exit before the LDS merge below is uniform over a row, so with
-  // RW = 4 the whole workgroup leaves together.
-  if (rowi >= P.batch * P.hq) return;
-  const int b = rowi / P.hq, h = rowi % P.hq;
-  // The ranges w0..w1 whose pages include sequence b's, and whether b is
-  // range w0's first sequence (w0_off = 0) or a later one (w0_off = 1).
-  int np, w0, w1, w0_off;
+  // Row (b, h) of the output, the ranges w0..w1 whose pages include
+  // sequence b's, and whether b is range w0's first sequence (w0_off = 0)
+  // or a later one (w0_off = 1).
+  int b, h, np, w0, w1, w0_off;
   if constexpr (META) {
-    // One round: b's length and the ranges' records.  The ranges whose
-    // first sequence is b are r1..r2; b began in range r1 - 1 if r1 starts
-    // inside it, else in r1.
-    np = seq_pages(P, b);
-    constexpr int U = 8;
-    int r1 = -1, r2 = -1, inside = 0;
-    for (int base = 0; base < P.nwg; base += 64 * U) {
-      int mv[U];
+    // One row per (range boundary r, head): the sequence that range r starts
+    // inside, merged at the first boundary that cuts it.  Every other
+    // sequence either ends inside one range (written directly) or is empty;
+    // the workgroups past the rows give the empty ones zeros.
+    static_assert(RW == 1, "range records come with more than 64 sequences");
+    const int nrw = ((P.nwg - 1) * P.hq + 3) / 4;
+    if ((int)blockIdx.x >= nrw) {
+      const int base = ((int)blockIdx.x - nrw) * 256 + wave * 64;
+      const int i = base + lane;
+      unsigned long long empty =
+          __builtin_amdgcn_ballot_w64(i < P.batch && seq_pages(P, min(i, P.batch - 1)) == 0);
+      while (empty) {
+        const int e = base + __builtin_ffsll((long long)empty) - 1;
+        empty &= empty - 1;
+        for (int hh = 0; hh < P.hq; ++hh) {
 #pragma unroll
-      for (int u = 0; u < U; ++u) mv[u] = P.range_meta[min(base + 64 * u + lane, P.nwg - 1)];
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int r = base + 64 * u + lane;
-        const unsigned long long hit = __builtin_amdgcn_ballot_w64(r < P.nwg && mv[u] >> 1 == b);
-        if (hit) {
-          const int lo = __builtin_ffsll((long long)hit) - 1;
-          if (r1 < 0) {
-            r1 = base + 64 * u + lo;
-            inside = __builtin_amdgcn_readlane(mv[u], lo) & 1;
-          }
-          r2 = base + 64 * u + 63 - __builtin_clzll(hit);
+          for (int j = 0; j < PER; ++j)
+            store_out<OutT>(P.out, ((size_t)e * P.hq + hh) * D + lane + 64 * j, 0.f);
         }
       }
+      return;
     }
-    w0 = r1 < 0 ? 0 : r1 - inside;
-    w1 = r1 < 0 ? 0 : r2;  // no range starts in b: b lies inside one range
-    w0_off = inside;
+    const int rowi = blockIdx.x * 4 + wave;
+    const int r = 1 + rowi / P.hq;
+    h = rowi % P.hq;
+    if (r >= P.nwg) return;
+    const int m1 = P.range_meta[r], m0 = P.range_meta[r - 1];
+    b = m1 >> 1;
+    if (!(m1 & 1)) return;                       // r starts on a sequence's first page
+    if (m0 >> 1 == b && (m0 & 1)) return;        // an earlier boundary cuts b too
+    w0 = r - 1;
+    w0_off = m0 >> 1 == b ? 0 : 1;
+    // The ranges after r that start inside b follow r: count them.
+    w1 = r;
+    for (int base = r + 1; base < P.nwg; base += 64) {
+      const int rr = base + lane;
+      const int mv = P.range_meta[min(rr, P.nwg - 1)];
+      const unsigned long long hit = __builtin_amdgcn_ballot_w64(rr < P.nwg && mv >> 1 == b);
+      const int n = ~hit ? __builtin_ffsll((long long)~hit) - 1 : 64;
+      w1 += n;
+      if (n < 64) break;
+    }
+    np = 1;
   } else {
+    const int rowi = blockIdx.x * (4 / RW) + wave / RW;
+    // Every exit before the LDS merge below is uniform over a row, so with
+    // RW = 4 the whole workgroup leaves together.
+    if (rowi >= P.batch * P.hq) return;
+    b = rowi / P.hq;
+    h = rowi % P.hq;
     // Lengths of the whole batch, 64 per round: the page total (as
     // flat_range), the pages before sequence b and b's own page count.
     int total = 0, before = 0;
@@ -653,7 +671,8 @@ __global__ __launch_bounds__(256) void merge_kernel(AttnParams P) {
   if (np == 0) {
     if (sub == 0) {
 #pragma unroll
-      for (int j = 0; j < PER; ++j) store_out<OutT>(P.out, (size_t)rowi * D + lane + 64 * j, 0.f);
+      for (int j = 0; j < PER; ++j)
+        store_out<OutT>(P.out, ((size_t)b * P.hq + h) * D + lane + 64 * j, 0.f);
     }
     return;
   }
@@ -745,7 +764,7 @@ __global__ __launch_bounds__(256) void merge_kernel(AttnParams P) {
   const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
 #pragma unroll
   for (int j = 0; j < PER; ++j)
-    store_out<OutT>(P.out, (size_t)rowi * D + lane + 64 * j, a[j] * inv);
+    store_out<OutT>(P.out, ((size_t)b * P.hq + h) * D + lane + 64 * j, a[j] * inv);
 }
 
 }  // namespace
@@ -777,14 +796,17 @@ hipError_t launch_dim(const AttnParams& P, bool vec, hipStream_t st) {
   const unsigned rows = (unsigned)P.batch * P.hq;
   // Four waves per row once the ranges outnumber the sequences 16 to 1
   // (never with pair slots, which need more sequences than ranges).
-  // Range records come with more than 64 sequences (below, RW = 1).
+  // Range records come with more than 64 sequences (below, RW = 1): a row
+  // per (range boundary, head), then a workgroup per 256 sequences for the
+  // empty ones.
   const dim3 g1((rows + 3) / 4);
+  const dim3 gm((unsigned)((((size_t)P.nwg - 1) * P.hq + 3) / 4 + ((size_t)P.batch + 255) / 256));
   if (P.nwg >= 16 * P.batch)
     merge_kernel<D, OutT, 4, false, false><<<dim3(rows), 256, 0, st>>>(P);
   else if (P.range_meta && P.pair_slots)
-    merge_kernel<D, OutT, 1, true, true><<<g1, 256, 0, st>>>(P);
+    merge_kernel<D, OutT, 1, true, true><<<gm, 256, 0, st>>>(P);
   else if (P.range_meta)
-    merge_kernel<D, OutT, 1, false, true><<<g1, 256, 0, st>>>(P);
+    merge_kernel<D, OutT, 1, false, true><<<gm, 256, 0, st>>>(P);
   else if (P.pair_slots)
     merge_kernel<D, OutT, 1, true, false><<<g1, 256, 0, st>>>(P);
   else
