@@ -706,14 +706,24 @@ __global__ __launch_bounds__(256) void merge_kernel(AttnParams P) {
     // the partial loads do not depend on the weights.
     const size_t r = (size_t)slot_of(wb + min(lane, cnt - 1)) * P.hq + h;
     const float mp0 = P.part_ml[2 * r], lp0 = P.part_ml[2 * r + 1];
-    float v[8][PER];
-    load8p(wb, cnt, 0, v);
-    // One wait for both load sets here; left alone, the compiler sinks the
-    // partial loads below the reductions and pays a second round trip.
+    // Up to S steps of eight partials load together with them (a wave of
+    // a four-wave row over one long sequence combines 32).
+    constexpr int S = 4;
+    float v[S][8][PER];
+    load8p(wb, cnt, 0, v[0]);
 #pragma unroll
-    for (int u = 0; u < 8; ++u)
+    for (int k = 1; k < S; ++k)
+      if (8 * k < cnt) load8p(wb, cnt, 8 * k, v[k]);
+    // One wait for all the load sets here; left alone, the compiler sinks
+    // the partial loads below the reductions and pays a round trip each.
 #pragma unroll
-      for (int j = 0; j < PER; ++j) asm volatile("" ::"v"(v[u][j]));
+    for (int k = 0; k < S; ++k)
+      if (k == 0 || 8 * k < cnt) {
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+#pragma unroll
+          for (int j = 0; j < PER; ++j) asm volatile("" ::"v"(v[k][u][j]));
+      }
     const float mp = lane < cnt ? mp0 : kNegInf;
     const float lp = lane < cnt ? lp0 : 0.f;
     const float mn = __builtin_fmaxf(mm, wave_max(mp));
@@ -724,15 +734,21 @@ __global__ __launch_bounds__(256) void merge_kernel(AttnParams P) {
 #pragma unroll
     for (int j = 0; j < PER; ++j) a[j] *= a1;
     mm = mn;
-    for (int i0 = 0; i0 < cnt; i0 += 8) {
-      if (i0 > 0) load8p(wb, cnt, i0, v);
+    auto add8 = [&](int i0, const float (&vs)[8][PER]) {
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
         const float wi = __builtin_bit_cast(
             float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), min(i0 + u, 63)));
 #pragma unroll
-        for (int j = 0; j < PER; ++j) a[j] += wi * v[u][j];
+        for (int j = 0; j < PER; ++j) a[j] += wi * vs[u][j];
       }
+    };
+#pragma unroll
+    for (int k = 0; k < S; ++k)
+      if (8 * k < cnt) add8(8 * k, v[k]);
+    for (int i0 = 8 * S; i0 < cnt; i0 += 8) {
+      load8p(wb, cnt, i0, v[0]);
+      add8(i0, v[0]);
     }
   }
   if constexpr (RW > 1) {
