@@ -864,10 +864,22 @@ long long zdim_of(const bc_shape& s) {
 // block (zdim waves), and kMaxWaves waves per CU keep the most bytes in
 // flight (same box, 32/8 heads: one wave more per SIMD measured 5 % slower
 // at 64 sequences; at 1-2 head blocks, one workgroup per CU left the CUs
-// 16-45 % slower than four waves each).
+// 16-45 % slower than four waves each).  D = 64 pages carry half the bytes,
+// so twice the ranges (eight waves per CU) keep as many in flight: 64
+// sequences of up to 4096 tokens 67.1 -> 50.8 us, 128 of them 121.1 -> 92.4.
 int flat_ranges(const bc_shape& s, int cus) {
-  const long long n = (long long)(cus > 0 ? cus : 256) * kMaxWaves / zdim_of(s);
+  const long long n =
+      (long long)(cus > 0 ? cus : 256) * kMaxWaves * (s.dim == 64 ? 2 : 1) / zdim_of(s);
   return n < 1 ? 1 : n > (1 << 20) ? (1 << 20) : (int)n;
+}
+
+// The ranges a launch uses: flat_ranges, but at least two pages per range
+// on a full page table (one 4096-token sequence over 256 ranges of one page
+// merged 256 partials per row: 11.96 against 10.40 us at 128 ranges).
+int launch_ranges(const bc_shape& s, int cus) {
+  const long long cap = (long long)s.batch * s.max_pages / 2;
+  const int r = flat_ranges(s, cus);
+  return cap < 1 ? 1 : cap < r ? (int)cap : r;
 }
 
 // Flat-mode workgroup count for bc_decode's `slots` partial slots per head:
@@ -882,7 +894,7 @@ int flat_workgroups(int batch, long long slots, int ranges) {
 }
 
 // Packed decode with a workspace: one wave of flat ranges.
-int packed_nwg(const bc_shape& s) { return flat_ranges(s, device_cus()); }
+int packed_nwg(const bc_shape& s) { return launch_ranges(s, device_cus()); }
 
 // Partial slots per head: nwg + batch with slot = range + sequence, or two
 // per range once the batch outnumbers the ranges (AttnParams::pair_slots).
@@ -928,7 +940,7 @@ extern "C" int bc_decode(bc_shape s, bc_inputs in, bc_scratch scratch,
   // partial slots fit the caller's splits*B*Hq rows.
   P.nwg = splits == 1 ? 0
                       : flat_workgroups(s.batch, (long long)splits * s.batch,
-                                        flat_ranges(s, device_cus()));
+                                        launch_ranges(s, device_cus()));
   // Above 64 sequences the range records go to the (max, sum) scratch past
   // the slots in use where it has room for them; otherwise the merge kernel
   // finds the ranges from the lengths.

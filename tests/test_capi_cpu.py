@@ -217,10 +217,11 @@ def test_packed_workspace_fits_a_pool_slot():
     for hq, hkv in ((128, 1), (128, 8), (64, 1), (32, 1), (16, 1), (8, 1), (32, 8), (48, 3),
                     (64, 64), (1, 1)):
         for batch in (1, 64, 1000, 100000):
-            need = lib.bc_packed_decode_workspace_size(capi.Shape(batch, hq, hkv, 128, 4096, 10**6))
-            worst = max(worst, need)
-            assert need <= capi.BC_SCRATCH_SLOT_BYTES, (hq, hkv, batch, need)
-    assert worst >= 128 * 256 * 130 * 4  # the bound is reached
+            for d in (64, 128):  # D = 64 runs twice the ranges at half the slot size
+                need = lib.bc_packed_decode_workspace_size(capi.Shape(batch, hq, hkv, d, 4096, 10**6))
+                worst = max(worst, need)
+                assert need <= capi.BC_SCRATCH_SLOT_BYTES, (hq, hkv, batch, d, need)
+    assert worst >= 128 * 256 * 130 * 4  # the D = 128 bound is reached
 
 
 def test_auto_splits_policy():

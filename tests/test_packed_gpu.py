@@ -211,19 +211,20 @@ PAIR_CASES = {
     "3-page-sequences": (32, 8, 128, lambda rng: np.full(200, 48)),
     "ragged-with-empties": (32, 8, 128, lambda rng: np.where(np.arange(300) % 7 == 0, 0,
                                                              rng.integers(1, 601, size=300))),
-    # three head blocks: 341 ranges; four: 256; 32 (no grouping): 32
-    "three-head-blocks": (48, 3, 64, lambda rng: rng.integers(0, 201, size=500)),
+    # three head blocks: 341 ranges; four: 256; 32 (no grouping): 32, or 64
+    # at D = 64 (twice the ranges)
+    "three-head-blocks": (48, 3, 128, lambda rng: rng.integers(0, 201, size=500)),
     "four-head-blocks": (32, 4, 128, lambda rng: rng.integers(1, 301, size=400)),
     "32-head-blocks": (32, 32, 64, lambda rng: rng.integers(0, 501, size=100)),
     # at most 64 sequences: the merge finds the ranges from the lengths
-    "32-head-blocks-60": (32, 32, 64, lambda rng: rng.integers(0, 301, size=60)),
+    "32-head-blocks-60": (32, 32, 128, lambda rng: rng.integers(0, 301, size=60)),
 }
 
 
 @pytest.mark.parametrize("case", list(PAIR_CASES))
 def test_batches_above_the_ranges_use_pair_slots(case, oracle):
-    """Batches of more sequences than flat ranges (4 * CUs / head blocks)
-    split at any context length, with two partial slots per range: a
+    """Batches of more sequences than flat ranges (4 * CUs / head blocks,
+    twice that at D = 64) split at any context length, with two partial slots per range: a
     workspace of 2 * ranges slots whatever the batch.  The workspace call
     and the reference-signature call (its scratch a slot of the library's
     pool, where the workspace fits one) give the same bits, within the
@@ -234,7 +235,8 @@ def test_batches_above_the_ranges_use_pair_slots(case, oracle):
     q, cache, strides, NB, pages, lens = _packed_fixture(rng, make(rng), hq, hkv, d)
     B = len(lens)
     zdim = hkv * -(-(hq // hkv) // 16)
-    ranges = 4 * torch.cuda.get_device_properties(0).multi_processor_count // zdim
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    ranges = 4 * cus * (2 if d == 64 else 1) // zdim
     assert B > ranges
     need = G.lib().bc_packed_decode_workspace_size(capi.Shape(B, hq, hkv, d, pages.shape[1], NB))
     assert need == 2 * ranges * hq * (d + 2) * 4 + ranges * 4, need
