@@ -44,9 +44,9 @@ sys.path.insert(0, str(ROOT / "branchcraft-cuda_amd" / "python"))
 
 HBM_PEAK_GBS = 8000.0
 # HBM bytes per config-5 call measured with rocprofv3 counters: attention
-# FETCH 264,747.1 KiB x 2 + WRITE 3,021.5 KiB, merge FETCH 1,573.5 KiB x 2 +
+# FETCH 264,747.3 KiB x 2 + WRITE 3,021.5 KiB, merge FETCH 1,595.0 KiB x 2 +
 # WRITE 448.0 KiB (FETCH_SIZE reads half of a 512 MiB copy's bytes).
-C5_HBM_TRAFFIC_BYTES = (264748.7 * 2 + 3021.5 + 1581.5 * 2 + 448.0) * 1024
+C5_HBM_TRAFFIC_BYTES = (264747.3 * 2 + 3021.5 + 1595.0 * 2 + 448.0) * 1024
 MFMA_F16_PEAK_TFLOPS = 2500.0
 PAGE = 16
 

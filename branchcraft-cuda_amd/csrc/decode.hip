@@ -957,7 +957,7 @@ extern "C" int bc_auto_splits(bc_shape s, int max_length, int cu_count) {
   // splits == 1 runs one workgroup per (sequence, head block) with the pages
   // split kSlices ways inside it and no merge kernel.  splits > 1 runs flat
   // page ranges, min((splits - 1) * batch + 1, R) of them, R = flat_ranges
-  // (one wave of workgroups at four waves per CU).
+  // (one wave of workgroups at four waves per CU, eight at D = 64).
   //  - With one or two head blocks, batches whose (sequence, head block)
   //    workgroups fill the CUs stay whole: eight waves per CU beat the
   //    ranges' four there (same box, 1024 tokens: 8/1 heads, 512 sequences

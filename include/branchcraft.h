@@ -114,7 +114,8 @@ typedef struct bc_tree_inputs {
  * block), its waves splitting the pages and merging in LDS, with no scratch.
  * splits > 1 spreads the batch's pages over equal ranges of the concatenated
  * sequences, at most (splits - 1) * B + 1 of them and at most one wave of
- * workgroups (4 * CUs / head blocks ranges), and merges the FP32
+ * workgroups (R = 4 * CUs / head blocks ranges, twice that at dim 64, and
+ * at most half the table's pages), and merges the FP32
  * partial softmax states of the sequences a range boundary cuts; the
  * partials fit the reference's scratch sizes for `splits`.  FP16 tensors
  * that are not 16-byte aligned are read with 2-byte loads.
@@ -128,8 +129,9 @@ int bc_decode(bc_shape shape, bc_inputs in, bc_scratch scratch, int splits,
 /* Split-count heuristic for bc_decode on a device with `cu_count` compute
  * units; returns a value in [1, BC_MAX_SPLITS]: 1 with one or two head
  * blocks once batch * head blocks >= cu_count; else 2 for batches of at
- * least one wave of flat ranges (4 * cu_count / head blocks: 128 sequences
- * at 8 KV heads of 4 query heads on 256 CUs) at any length; else 1 for
+ * least one wave of flat ranges (4 * cu_count / head blocks, twice that at
+ * dim 64: 128 sequences at 8 KV heads of 4 query heads and dim 128 on 256
+ * CUs) at any length; else 1 for
  * max_length < 512.
  * Replaces branchcraft::auto_splits, include/branchcraft.hpp:41
  * (src/paged_gqa.cu:134-142), retuned for 256-CU MI355X workgroups: unlike
@@ -242,7 +244,8 @@ int bc_packed_decode(bc_shape shape, const bc_half* q, const bc_half* packed_kv,
 
 /* Bytes of workspace bc_packed_decode_ws needs for this shape: FP32
  * partials of min(R + B, 2R) slots of Hq * (D + 2) floats and one int per
- * range, R = 4 * CUs / head blocks flat ranges.  0 when bc_auto_splits, given the table's
+ * range, R = 4 * CUs / head blocks flat ranges (twice that at dim 64, at
+ * most half of batch * max_pages).  0 when bc_auto_splits, given the table's
  * capacity (max_pages * 16 tokens), keeps the shape unsplit: one or two
  * head blocks whose (sequence, head block) workgroups fill the CUs; a batch
  * below R with a table under 512 tokens, one of at most 768 tokens whose
@@ -252,14 +255,13 @@ int bc_packed_decode(bc_shape shape, const bc_half* q, const bc_half* packed_kv,
 size_t bc_packed_decode_workspace_size(bc_shape shape);
 
 /* bc_packed_decode with the batch's pages spread over equal ranges of the
- * concatenated sequences, one wave of workgroups (four waves per CU), and
- * an FP32 merge of the
- * sequences a range boundary cuts.  The workgroup count and the workspace
- * size depend on the shape and the device's CU count only; the kernels find
- * the ranges from the lengths on the device, so no lengths are read on the
- * host.  A null workspace, one smaller than required or not aligned to 16
- * bytes is ignored and the call is bc_packed_decode's; a shape whose
- * workspace size is 0 runs unsplit. */
+ * concatenated sequences, one wave of workgroups (four waves per CU, eight
+ * at dim 64), and an FP32 merge of the sequences a range boundary cuts.
+ * The workgroup count and the workspace size depend on the shape and the
+ * device's CU count only; the kernels find the ranges from the lengths on
+ * the device, so no lengths are read on the host.  A null workspace, one
+ * smaller than required or not aligned to 16 bytes is ignored and the call
+ * is bc_packed_decode's; a shape whose workspace size is 0 runs unsplit. */
 int bc_packed_decode_ws(bc_shape shape, const bc_half* q,
                         const bc_half* packed_kv, const int32_t* pages,
                         const int32_t* lengths, bc_half* output,
