@@ -87,7 +87,8 @@ struct AttnParams {
   int pair_slots;         // partial slot of range r cutting sequence b:
                           // 0: r + b (nwg + batch slots); 1: 2r for the
                           // range's first sequence, 2r + 1 for a later one
-                          // (2 * nwg slots, for batches above nwg)
+                          // (2 * nwg slots; packed decode above 64 sequences
+                          // under four ranges each, merged per range boundary)
 };
 
 // Every kernel argument into scalar registers at the kernel's start, in one
@@ -582,31 +583,36 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == kMaxWaves ? 3 : 2) void paged_
 
 // Flat mode: out = sum_w 2^(m_w - M) a_w / sum_w 2^(m_w - M) l_w over the
 // workgroups whose ranges cut sequence b (src/paged_gqa.cu:76-106); empty
-// sequences give zeros.  RW waves per (b, h) output row (1 or 4), two
-// dependent memory rounds: the lengths (page geometry), then every partial's
-// (max, sum) together with the first eight partials' accumulators; lane i
-// holds partial i's weight and every lane accumulates its dims.  With RW = 4
-// each wave combines a contiguous quarter of the row's partials and wave 0
-// merges the four states through LDS: rows of a few long sequences have
-// hundreds of partials, too many for one wave.
+// sequences give zeros.  Lane i holds partial i's weight and every lane
+// accumulates its dims.  Three row forms:
+//  - per (b, h) row (META false), RW waves each (1 or 4): two dependent
+//    memory rounds, the lengths (page geometry), then every partial's (max,
+//    sum) together with the first eight partials' accumulators.  With RW = 4
+//    each wave combines a contiguous quarter of the row's partials and wave
+//    0 merges the four states through LDS: rows of a few long sequences have
+//    hundreds of partials, too many for one wave.
+//  - per (range boundary, h) row with range records (META) and pair slots
+//    (PAIR): one round, records and partials together.
+//  - the same rows with slot = range + sequence (META only, bc_decode above
+//    64 sequences): the records, then the partials.
 template <int D, typename OutT, int RW, bool PAIR, bool META>
 __global__ __launch_bounds__(256) void merge_kernel(AttnParams P) {
   pin_params(P);
   static_assert(RW == 1 || RW == 4, "one or four waves per row");
+  static_assert(META || !PAIR, "pair slots come with range records");
   constexpr int PER = D / 64;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int sub = wave % RW;  // this wave's share of the row's partials
-  // Row (b, h) of the output, the ranges w0..w1 whose pages include
-  // sequence b's, and whether b is range w0's first sequence (w0_off = 0)
-  // or a later one (w0_off = 1).
-  int b, h, np, w0, w1, w0_off;
+  // Row (b, h) of the output and the ranges w0..w1 whose pages include
+  // sequence b's (slot w + b each).
+  int b, h, np, w0, w1;
   if constexpr (META) {
     // One row per (range boundary r, head): the sequence that range r starts
     // inside, merged at the first boundary that cuts it.  Every other
     // sequence either ends inside one range (written directly) or is empty;
     // the workgroups past the rows give the empty ones zeros.
-    static_assert(RW == 1, "range records come with more than 64 sequences");
+    static_assert(RW == 1, "one wave per boundary row");
     const int nrw = ((P.nwg - 1) * P.hq + 3) / 4;
     if ((int)blockIdx.x >= nrw) {
       const int base = ((int)blockIdx.x - nrw) * 256 + wave * 64;
@@ -628,12 +634,130 @@ __global__ __launch_bounds__(256) void merge_kernel(AttnParams P) {
     const int r = 1 + rowi / P.hq;
     h = rowi % P.hq;
     if (r >= P.nwg) return;
+    if constexpr (PAIR) {
+      // Pair slots: boundary r's parts are ranges r - 1 + p.  Part p >= 1
+      // starts inside the row's sequence (slot 2(r - 1 + p)); part 0 holds it
+      // as its first sequence (slot 2(r - 1)) or a later one (2(r - 1) + 1).
+      // No slot depends on which sequence that is, so the records, every
+      // part's (max, sum), both part-0 candidates and the first KP parts'
+      // accumulators go out in one memory round, before the row knows
+      // whether it merges at all.
+      constexpr int KP = 4;
+      auto srow = [&](int slot) { return (size_t)slot * P.hq + h; };
+      const int m1 = P.range_meta[r], m0 = P.range_meta[r - 1];
+      const int mv = P.range_meta[min(r + 1 + lane, P.nwg - 1)];  // range r + 1 + lane
+      const size_t rl = srow(2 * min(r - 1 + lane, P.nwg - 1));
+      const float mpa = P.part_ml[2 * rl], lpa = P.part_ml[2 * rl + 1];
+      const size_t rb = srow(2 * (r - 1) + 1);
+      const float mpb = P.part_ml[2 * rb], lpb = P.part_ml[2 * rb + 1];
+      float va[KP][PER], vb[PER];
+#pragma unroll
+      for (int k = 0; k < KP; ++k) {
+        const float* src = P.part_acc + srow(2 * min(r - 1 + k, P.nwg - 1)) * D + lane;
+#pragma unroll
+        for (int j = 0; j < PER; ++j) va[k][j] = src[64 * j];
+      }
+#pragma unroll
+      for (int j = 0; j < PER; ++j) vb[j] = P.part_acc[rb * D + lane + 64 * j];
+      // Every load above is issued before the first use (otherwise the
+      // compiler sinks the accumulator loads below the branches).
+      asm volatile("" ::"v"(mv), "v"(mpa), "v"(lpa), "v"(mpb), "v"(lpb));
+#pragma unroll
+      for (int j = 0; j < PER; ++j) {
+        asm volatile("" ::"v"(vb[j]));
+#pragma unroll
+        for (int k = 0; k < KP; ++k) asm volatile("" ::"v"(va[k][j]));
+      }
+      b = m1 >> 1;
+      if (!(m1 & 1)) return;                 // r starts on a sequence's first page
+      if (m0 >> 1 == b && (m0 & 1)) return;  // an earlier boundary cuts b too
+      const bool later = m0 >> 1 != b;       // part 0 in slot 2(r - 1) + 1
+      // The ranges after r whose first sequence is b follow r: count them.
+      w1 = r;
+      {
+        const unsigned long long hit =
+            __builtin_amdgcn_ballot_w64(r + 1 + lane < P.nwg && mv >> 1 == b);
+        const int n = ~hit ? __builtin_ffsll((long long)~hit) - 1 : 64;
+        w1 += n;
+        for (int base = r + 65; n == 64 && base < P.nwg; base += 64) {
+          const int rr = base + lane;
+          const int mw = P.range_meta[min(rr, P.nwg - 1)];
+          const unsigned long long more = __builtin_amdgcn_ballot_w64(rr < P.nwg && mw >> 1 == b);
+          const int k = ~more ? __builtin_ffsll((long long)~more) - 1 : 64;
+          w1 += k;
+          if (k < 64) break;
+        }
+      }
+      const int nparts = w1 - r + 2;
+      float mm = kNegInf, lsum = 0.f, a[PER];
+#pragma unroll
+      for (int j = 0; j < PER; ++j) a[j] = 0.f;
+      for (int c0 = 0; c0 < nparts; c0 += 64) {
+        const int cnt = min(64, nparts - c0);
+        float mp, lp;
+        if (c0 == 0) {
+          mp = lane == 0 && later ? mpb : mpa;
+          lp = lane == 0 && later ? lpb : lpa;
+        } else {
+          const size_t rr = srow(2 * min(r - 1 + c0 + lane, P.nwg - 1));
+          mp = P.part_ml[2 * rr];
+          lp = P.part_ml[2 * rr + 1];
+        }
+        mp = lane < cnt ? mp : kNegInf;
+        lp = lane < cnt ? lp : 0.f;
+        const float mn = __builtin_fmaxf(mm, wave_max(mp));
+        const float ms = safe_max(mn);
+        const float a1 = fast_exp2(mm - ms);
+        const float w = fast_exp2(mp - ms);  // 0 past the parts
+        lsum = lsum * a1 + wave_sum(w * lp);
+#pragma unroll
+        for (int j = 0; j < PER; ++j) a[j] *= a1;
+        mm = mn;
+        auto wt = [&](int p) {
+          return __builtin_bit_cast(
+              float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), p));
+        };
+        int i0 = 0;
+        if (c0 == 0) {
+#pragma unroll
+          for (int k = 0; k < KP; ++k)
+            if (k < cnt) {
+              const float wk = wt(k);
+#pragma unroll
+              for (int j = 0; j < PER; ++j) a[j] += wk * (k == 0 && later ? vb[j] : va[k][j]);
+            }
+          i0 = KP;
+        }
+        // The rest eight parts per step (slots past cnt re-read the last
+        // part, with weight 0).
+        for (int i = i0; i < cnt; i += 8) {
+          float v[8][PER];
+#pragma unroll
+          for (int u = 0; u < 8; ++u) {
+            const int p = min(i + u, cnt - 1);
+            const float* src = P.part_acc + srow(2 * (r - 1 + c0 + p)) * D + lane;
+#pragma unroll
+            for (int j = 0; j < PER; ++j) v[u][j] = src[64 * j];
+          }
+#pragma unroll
+          for (int u = 0; u < 8; ++u) {
+            const float wu = i + u < cnt ? wt(i + u) : 0.f;
+#pragma unroll
+            for (int j = 0; j < PER; ++j) a[j] += wu * v[u][j];
+          }
+        }
+      }
+      const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+#pragma unroll
+      for (int j = 0; j < PER; ++j)
+        store_out<OutT>(P.out, ((size_t)b * P.hq + h) * D + lane + 64 * j, a[j] * inv);
+      return;
+    }
     const int m1 = P.range_meta[r], m0 = P.range_meta[r - 1];
     b = m1 >> 1;
     if (!(m1 & 1)) return;                       // r starts on a sequence's first page
     if (m0 >> 1 == b && (m0 & 1)) return;        // an earlier boundary cuts b too
     w0 = r - 1;
-    w0_off = m0 >> 1 == b ? 0 : 1;
     // The ranges after r that start inside b follow r: count them.
     w1 = r;
     for (int base = r + 1; base < P.nwg; base += 64) {
@@ -666,7 +790,6 @@ __global__ __launch_bounds__(256) void merge_kernel(AttnParams P) {
     const int per = max(1, (total + P.nwg - 1) / P.nwg);
     w0 = before / per;
     w1 = np > 0 ? (before + np - 1) / per : w0;
-    w0_off = w0 * per < before ? 1 : 0;
   }
   if (np == 0) {
     if (sub == 0) {
@@ -677,12 +800,7 @@ __global__ __launch_bounds__(256) void merge_kernel(AttnParams P) {
     return;
   }
   if (w0 == w1) return;  // the sequence ended inside one range: written directly
-  // Range w's partial slot (AttnParams::pair_slots).  With pair slots, b is
-  // the first sequence of every range w0 < w <= w1 (they start on its
-  // pages), and of range w0 only if w0 starts on b's first page.
-  // PAIR = pair_slots, a template argument: the slot arithmetic sits in the
-  // address of every partial load below, ahead of the row's memory round.
-  auto slot_of = [&](int w) { return PAIR ? 2 * w + w0_off * (w == w0) : w + b; };
+  auto slot_of = [&](int w) { return w + b; };  // range w's partial slot
   // This wave's partials: [r0, r1] (empty when r1 < r0).
   const int nparts = w1 - w0 + 1;
   const int r0 = w0 + sub * nparts / RW, r1 = w0 + (sub + 1) * nparts / RW - 1;
@@ -823,8 +941,6 @@ hipError_t launch_dim(const AttnParams& P, bool vec, hipStream_t st) {
     merge_kernel<D, OutT, 1, true, true><<<gm, 256, 0, st>>>(P);
   else if (P.range_meta)
     merge_kernel<D, OutT, 1, false, true><<<gm, 256, 0, st>>>(P);
-  else if (P.pair_slots)
-    merge_kernel<D, OutT, 1, true, false><<<g1, 256, 0, st>>>(P);
   else
     merge_kernel<D, OutT, 1, false, false><<<g1, 256, 0, st>>>(P);
   return hipGetLastError();
@@ -896,10 +1012,23 @@ int flat_workgroups(int batch, long long slots, int ranges) {
 // Packed decode with a workspace: one wave of flat ranges.
 int packed_nwg(const bc_shape& s) { return launch_ranges(s, device_cus()); }
 
-// Partial slots per head: nwg + batch with slot = range + sequence, or two
-// per range once the batch outnumbers the ranges (AttnParams::pair_slots).
+// Packed decode's partial slots: above 64 sequences, while the ranges number
+// under four per sequence, pair slots (AttnParams::pair_slots, 2 * nwg
+// slots): the merge then takes one wave per range boundary and loads a row's
+// records and first partials in one round, their addresses not depending on
+// the sequence (same box, 32/8 heads, against records then partials: 512 x
+// U[16, 512] 101.3 -> 100.7-101.1 us, 2048 x U[16, 128] 140.4 -> 139.9-140.3
+// us).  Otherwise slot = range + sequence (nwg + batch slots), merged per
+// (sequence, head) row: up to 64 sequences it finds the ranges from one round
+// of lengths (C5 timed level either way), and with many ranges per sequence
+// the boundary rows' first round covers too few of a row's partials (16 x
+// U[128, 4096]: 30.9 against 31.5 us).
+bool packed_pairs(const bc_shape& s, int nwg) {
+  return s.batch > 64 && nwg < 4LL * s.batch;
+}
+
 size_t packed_slots(const bc_shape& s, int nwg) {
-  return s.batch > nwg ? 2 * (size_t)nwg : (size_t)nwg + s.batch;
+  return packed_pairs(s, nwg) ? 2 * (size_t)nwg : (size_t)nwg + s.batch;
 }
 
 // Workspace: partial accumulators (256-byte aligned), then their (max, sum)
@@ -1048,15 +1177,17 @@ static int packed_common(bc_shape s, const bc_half* q, const bc_half* kv,
   const size_t need = packed_workspace(s, nwg);
   if (ws && ws_bytes >= need && aligned16(ws) && packed_split(s)) {
     P.nwg = nwg;
-    P.pair_slots = s.batch > nwg ? 1 : 0;
+    P.pair_slots = packed_pairs(s, nwg) ? 1 : 0;
     const size_t slots = packed_slots(s, nwg);
     const size_t acc_bytes =
         (slots * s.query_heads * s.dim * sizeof(float) + 255) & ~(size_t)255;
     P.part_acc = static_cast<float*>(ws);
     P.part_ml = reinterpret_cast<float*>(static_cast<char*>(ws) + acc_bytes);
-    // Up to 64 sequences the merge kernel reads every length in one round
-    // anyway; the range records pay from there on.
-    if (s.batch > 64) P.range_meta = reinterpret_cast<int*>(P.part_ml + slots * s.query_heads * 2);
+    // Range records: with pair slots (the merge's boundary rows), and above
+    // 64 sequences, where the per-row merge would scan the lengths 64 per
+    // round.
+    if (P.pair_slots || s.batch > 64)
+      P.range_meta = reinterpret_cast<int*>(P.part_ml + slots * s.query_heads * 2);
   }
   return launch<_Float16>(P, s.dim, reinterpret_cast<hipStream_t>(stream));
 }

@@ -298,10 +298,13 @@ def test_workspace_sizes():
     assert lib.bc_packed_decode_workspace_size(capi.Shape(128, 32, 8, 128, 8, 64)) > 0
     assert lib.bc_packed_decode_workspace_size(capi.Shape(64, 32, 8, 128, 32, 64)) > 0
     # Partial slots per head: ranges + batch (C5: 128 + 64), or two per range
-    # once the batch outnumbers the ranges, whatever the batch; then one
-    # int per range for the merge kernel.
+    # above 64 sequences while the ranges number under four per sequence,
+    # whatever the batch; then one int per range for the merge kernel.
     row = 32 * (128 + 2) * 4  # one slot of every head: acc and (max, sum)
     assert lib.bc_packed_decode_workspace_size(c5) == (128 + 64) * row + 128 * 4
+    for batch in (65, 100, 128):
+        mid = capi.Shape(batch, 32, 8, 128, 64, 70000)
+        assert lib.bc_packed_decode_workspace_size(mid) == 2 * 128 * row + 128 * 4, batch
     for batch in (129, 1024, 65536):
         big = capi.Shape(batch, 32, 8, 128, 64, 70000)
         assert lib.bc_packed_decode_workspace_size(big) == 2 * 128 * row + 128 * 4, batch

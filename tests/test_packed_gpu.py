@@ -187,10 +187,10 @@ def test_large_batch_takes_split_path(oracle):
         assert np.all(err <= G.f16_tolerance(exp32, 2e-3)), f"ws={ws} max err {err.max():.3e}"
 
 
-def _packed_fixture(rng, lens, hq, hkv, d):
+def _packed_fixture(rng, lens, hq, hkv, d, min_pages=1):
     lens = np.asarray(lens, dtype=np.int32)
     B = len(lens)
-    maxp = max(1, -(-int(lens.max()) // 16))
+    maxp = max(min_pages, -(-int(lens.max()) // 16))
     NB = sum(-(-int(n) // 16) for n in lens) + 8
     cache = torch.randn((NB, 2, 16, hkv, d), device="cuda", dtype=torch.float16)
     perm = rng.permutation(NB).astype(np.int32)
@@ -216,7 +216,8 @@ PAIR_CASES = {
     "three-head-blocks": (48, 3, 128, lambda rng: rng.integers(0, 201, size=500)),
     "four-head-blocks": (32, 4, 128, lambda rng: rng.integers(1, 301, size=400)),
     "32-head-blocks": (32, 32, 64, lambda rng: rng.integers(0, 501, size=100)),
-    # at most 64 sequences: the merge finds the ranges from the lengths
+    # at most 64 sequences: range + sequence slots, the merge finds the
+    # ranges from the lengths
     "32-head-blocks-60": (32, 32, 128, lambda rng: rng.integers(0, 301, size=60)),
 }
 
@@ -224,8 +225,9 @@ PAIR_CASES = {
 @pytest.mark.parametrize("case", list(PAIR_CASES))
 def test_batches_above_the_ranges_use_pair_slots(case, oracle):
     """Batches of more sequences than flat ranges (4 * CUs / head blocks,
-    twice that at D = 64) split at any context length, with two partial slots per range: a
-    workspace of 2 * ranges slots whatever the batch.  The workspace call
+    twice that at D = 64) split at any context length.  Above 64 sequences
+    they keep two partial slots per range, a workspace of 2 * ranges slots
+    whatever the batch; up to 64, ranges + batch slots.  The workspace call
     and the reference-signature call (its scratch a slot of the library's
     pool, where the workspace fits one) give the same bits, within the
     packed tolerance of the oracle."""
@@ -239,7 +241,8 @@ def test_batches_above_the_ranges_use_pair_slots(case, oracle):
     ranges = 4 * cus * (2 if d == 64 else 1) // zdim
     assert B > ranges
     need = G.lib().bc_packed_decode_workspace_size(capi.Shape(B, hq, hkv, d, pages.shape[1], NB))
-    assert need == 2 * ranges * hq * (d + 2) * 4 + ranges * 4, need
+    slots = 2 * ranges if B > 64 else ranges + B
+    assert need == slots * hq * (d + 2) * 4 + ranges * 4, need
     scale = 1 / math.sqrt(d)
     exp32, _ = oracle.packed_decode(q, cache.cpu().numpy(), pages, lens, strides, hkv, scale,
                                     threads=16)
@@ -251,6 +254,58 @@ def test_batches_above_the_ranges_use_pair_slots(case, oracle):
     if need <= capi.BC_SCRATCH_SLOT_BYTES:  # fits a pool slot: the same split
         assert np.array_equal(outs[0].view(np.uint16), outs[1].view(np.uint16))
     assert np.all(exp32[lens == 0] == 0) and np.all(outs[0][lens == 0] == 0)
+
+
+def _one_long(rng):
+    lens = rng.integers(0, 49, size=100)
+    lens[37] = 6000  # 375 pages of about 575: more than 64 of the 128 ranges
+    return lens
+
+
+MID_CASES = {
+    # 1-4 ranges per sequence (ranges of about 50 pages)
+    "100-uniform": (lambda rng: rng.integers(16, 2049, size=100), 1),
+    # one sequence cut by over 64 boundaries among short and empty ones
+    "100-one-long": (_one_long, 1),
+    # 128 sequences of 4 pages over 128 ranges of 4 pages: no range cuts a
+    # sequence, every boundary row leaves at its record
+    "128-aligned": (lambda rng: np.full(128, 64), 32),
+    "72-ragged-empties": (lambda rng: np.where(np.arange(72) % 5 == 0, 0,
+                                               rng.integers(1, 1500, size=72)), 1),
+}
+
+
+@pytest.mark.parametrize("case", list(MID_CASES))
+def test_batches_above_64_merge_per_range_boundary(case, oracle):
+    """Above 64 sequences, while the ranges number under four per sequence,
+    packed decode keeps two partial slots per range and its merge takes one
+    wave per range boundary, loading the range records, every part's (max,
+    sum) and the first parts' accumulators in one round.  Rows whose
+    sequence spans more parts than that round holds (over 64 here) load the
+    rest after it.  Both entry points give the same bits, within the packed
+    tolerance of the oracle; empty sequences give zeros."""
+    hq, hkv, d = 32, 8, 128
+    make, min_pages = MID_CASES[case]
+    rng = np.random.default_rng(len(case) + 100)
+    torch.manual_seed(len(case) + 100)
+    q, cache, strides, NB, pages, lens = _packed_fixture(rng, make(rng), hq, hkv, d,
+                                                          min_pages=min_pages)
+    B = len(lens)
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    ranges = 4 * cus // 8
+    assert 64 < B <= ranges < 4 * B
+    need = G.lib().bc_packed_decode_workspace_size(capi.Shape(B, hq, hkv, d, pages.shape[1], NB))
+    assert need == 2 * ranges * hq * (d + 2) * 4 + ranges * 4, need
+    scale = 1 / math.sqrt(d)
+    exp32, _ = oracle.packed_decode(q, cache.cpu().numpy(), pages, lens, strides, hkv, scale,
+                                    threads=16)
+    outs = [G.packed(q, cache, strides, hkv, NB, pages, lens, scale, workspace=ws)
+            for ws in (True, False)]
+    for ws, out in zip((True, False), outs):
+        err = np.abs(out.astype(np.float32) - exp32)
+        assert np.all(err <= G.f16_tolerance(exp32, 2e-3)), f"ws={ws} max err {err.max():.3e}"
+    assert np.array_equal(outs[0].view(np.uint16), outs[1].view(np.uint16))
+    assert np.all(outs[0][lens == 0] == 0)
 
 
 def test_misaligned_workspace_is_ignored():
