@@ -819,16 +819,18 @@ __global__ __launch_bounds__(64 * W, 2) void tree_split_kernel(TreeParams P) {
     }
     return ok;
   };
-  auto issue = [&](int idx, const int (&ph)[2]) {
+  // One tile's loads: K (is_v false), V (true), or both.
+  auto issue_part = [&](int idx, const int (&ph)[2], bool k, bool v) {
     if (tbeg + ln + LN * idx < ntd) {
-      issue_half(idx, ph, false, std::true_type{});
-      issue_half(idx, ph, true, std::true_type{});
+      if (k) issue_half(idx, ph, false, std::true_type{});
+      if (v) issue_half(idx, ph, true, std::true_type{});
     } else {
-      issue_half(idx, ph, false, std::false_type{});
-      issue_half(idx, ph, true, std::false_type{});
+      if (k) issue_half(idx, ph, false, std::false_type{});
+      if (v) issue_half(idx, ph, true, std::false_type{});
     }
-    rowok = rows_of(idx, ph);
+    if (v) rowok = rows_of(idx, ph);
   };
+  auto issue = [&](int idx, const int (&ph)[2]) { issue_part(idx, ph, true, true); };
 
   // first_tag: std::true_type for the wave's first tile (a separate copy
   // of the tile code), std::false_type for the rest.
@@ -870,6 +872,9 @@ __global__ __launch_bounds__(64 * W, 2) void tree_split_kernel(TreeParams P) {
     }
     wave_lds_sync();
     if (!first && idx + 1 < nmine) issue(idx + 1, next_ids);
+    // The first tile's K registers are free once K is staged: the next
+    // tile's K loads go out now, its V loads once this tile's V is staged.
+    if (first && idx + 1 < nmine) issue_part(idx + 1, next_ids, true, false);
     f16x8 pb[2], pl[2];
     if constexpr (QL)
       tile_scores<D, 64, first>(ks + lr * KP, s_q + (size_t)rq * KS * 64 + lane, okbits,
@@ -879,7 +884,7 @@ __global__ __launch_bounds__(64 * W, 2) void tree_split_kernel(TreeParams P) {
     if constexpr (first) {
       stage_v();
       wave_lds_sync();
-      if (idx + 1 < nmine) issue(idx + 1, next_ids);
+      if (idx + 1 < nmine) issue_part(idx + 1, next_ids, false, true);
     }
     tile_pv<D, first>(vtr, pb, pl, acc);
     // The staging area is rewritten by the next tile.
