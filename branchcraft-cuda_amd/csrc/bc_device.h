@@ -19,6 +19,20 @@ __device__ __forceinline__ float fast_exp2(float x) {
   return __builtin_amdgcn_exp2f(x);  // v_exp_f32; exp2(-inf) == 0
 }
 
+// FP16 hi/lo parts of two FP32 values, packed two per register (element 0
+// in the low half): hi = p truncated to FP16, lo = p - hi rounded to FP16, so
+// hi + lo carries about 21 bits of p.  Three instructions per pair: one
+// packed truncating conversion, then one mixed-precision FMA per half, which
+// reads hi's half as an FP16 operand, forms p - hi exactly in FP32 and writes
+// the FP16 result into its half of lo.
+__device__ __forceinline__ void split_hi_lo(float p0, float p1, uint32_t& hi, uint32_t& lo) {
+  hi = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(p0, p1));
+  asm("v_fma_mixlo_f16 %0, %1, -1.0, %2 op_sel_hi:[1,0,0]" : "=v"(lo) : "v"(hi), "v"(p0));
+  asm("v_fma_mixhi_f16 %0, %1, -1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
+      : "+v"(lo)
+      : "v"(hi), "v"(p1));
+}
+
 // DPP lane moves inside 16-lane rows (all rows and banks enabled).
 template <int CTRL>
 __device__ __forceinline__ float dpp_f(float x) {

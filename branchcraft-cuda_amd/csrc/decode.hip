@@ -25,7 +25,7 @@
 //       (D/32 x v_mfma_f32_16x16x32_f16; A operand lane = (token, 8-dim slice))
 //   O^T[D x 16 heads]     += V^T[D x 16 tok] . P^T[16 tok x 16 heads]
 //       (D/16 x v_mfma_f32_16x16x16_f16 for P's FP16 hi part and again for
-//        its lo part, so P keeps ~22 bits; the S^T accumulator is already the
+//        its lo part, so P keeps ~21 bits; the S^T accumulator is already the
 //        P^T B operand, lane for lane)
 //
 // Pages are fetched as whole token rows (each 16-byte load instruction covers
@@ -53,6 +53,7 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 // Up to four waves per workgroup at <= 168 VGPRs (three such workgroups fit
 // a CU).  Flat ranges launch one wave of workgroups, four waves per CU.
@@ -454,14 +455,19 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == kMaxWaves ? 3 : 2) void paged_
       m = mnew;
     }
     const float mc = safe_max(m) * c;
-    f16x4 ph, pl;
+    // P as an FP16 hi/lo pair (hi truncated, lo = p - hi rounded): P.V
+    // carries ~21 bits of P.
+    float pr[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const float pr = fast_exp2(__builtin_fmaf(sv[j], c, -mc));
-      l += pr;
-      ph[j] = (_Float16)pr;
-      pl[j] = (_Float16)(pr - (float)ph[j]);
+      pr[j] = fast_exp2(__builtin_fmaf(sv[j], c, -mc));
+      l += pr[j];
     }
+    uint32_t wh[2], wl[2];
+    split_hi_lo(pr[0], pr[1], wh[0], wl[0]);
+    split_hi_lo(pr[2], pr[3], wh[1], wl[1]);
+    const f16x4 ph = __builtin_bit_cast(f16x4, u32x2{wh[0], wh[1]});
+    const f16x4 pl = __builtin_bit_cast(f16x4, u32x2{wl[0], wl[1]});
 #pragma unroll
     for (int t = 0; t < DT; ++t) {
       const f16x4 a = lds_read_tr(vtr + 16 * t);

@@ -47,6 +47,7 @@ using namespace bcd;
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
@@ -311,16 +312,23 @@ __global__ __launch_bounds__(kThreads, 2) void tree_kernel(TreeParams P) {
       m = mnew;
     }
     // P is split into FP16 hi + lo parts (two MFMAs each) so the P.V product
-    // carries ~22 bits of P instead of FP16's 11.
+    // carries ~21 bits of P instead of FP16's 11.
     const float mb = safe_max(m);
     f16x8 pb[2], pl[2];
+    float pr[16];
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
-      const float pr = fast_exp2(sv[j] - mb);
-      l += pr;
-      const _Float16 hi = (_Float16)pr;
-      pb[j >> 3][j & 7] = hi;
-      pl[j >> 3][j & 7] = (_Float16)(pr - (float)hi);
+      pr[j] = fast_exp2(sv[j] - mb);
+      l += pr[j];
+    }
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      uint32_t wh[4], wl[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        split_hi_lo(pr[8 * hh + 2 * q], pr[8 * hh + 2 * q + 1], wh[q], wl[q]);
+      pb[hh] = __builtin_bit_cast(f16x8, u32x4{wh[0], wh[1], wh[2], wh[3]});
+      pl[hh] = __builtin_bit_cast(f16x8, u32x4{wl[0], wl[1], wl[2], wl[3]});
     }
 
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -540,17 +548,23 @@ __device__ __forceinline__ void tile_scores(const _Float16* kr, const uint4* qf,
       m = mnew;
     }
   }
-  // P splits into an FP16 hi part -- p with the low 13 mantissa bits
-  // cleared, exact in FP16 for p in [2^-14, 2^8] -- and lo = p - hi (exact
-  // in FP32, then rounded to FP16), so P.V carries ~21 bits of P.
+  // P splits into an FP16 hi part (p truncated to FP16, exact for p in
+  // [2^-14, 2^8]) and lo = p - hi rounded to FP16, so P.V carries ~21 bits
+  // of P.
   const float mb = safe_max(m);
+  float pr[16];
 #pragma unroll
   for (int j = 0; j < 16; ++j) {
-    const float pr = fast_exp2(__builtin_fmaf(sv[j], scale_log2, -mb));
-    l += pr;
-    const float hi = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, pr) & 0xffffe000u);
-    pb[j >> 3][j & 7] = (_Float16)hi;
-    pl[j >> 3][j & 7] = (_Float16)(pr - hi);
+    pr[j] = fast_exp2(__builtin_fmaf(sv[j], scale_log2, -mb));
+    l += pr[j];
+  }
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    uint32_t wh[4], wl[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) split_hi_lo(pr[8 * h + 2 * q], pr[8 * h + 2 * q + 1], wh[q], wl[q]);
+    pb[h] = __builtin_bit_cast(f16x8, u32x4{wh[0], wh[1], wh[2], wh[3]});
+    pl[h] = __builtin_bit_cast(f16x8, u32x4{wl[0], wl[1], wl[2], wl[3]});
   }
 }
 
@@ -1359,13 +1373,20 @@ __global__ __launch_bounds__(kThreads, 2) void tree_rows_kernel(TreeParams P) {
     }
     const float mb = safe_max(m);
     f16x8 pb[2], pl[2];
+    float pr[16];
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
-      const float pr = fast_exp2(__builtin_fmaf(svv[j], P.scale_log2, -mb));
-      l += pr;
-      const _Float16 hi = (_Float16)pr;
-      pb[j >> 3][j & 7] = hi;
-      pl[j >> 3][j & 7] = (_Float16)(pr - (float)hi);
+      pr[j] = fast_exp2(__builtin_fmaf(svv[j], P.scale_log2, -mb));
+      l += pr[j];
+    }
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      uint32_t wh[4], wl[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        split_hi_lo(pr[8 * hh + 2 * q], pr[8 * hh + 2 * q + 1], wh[q], wl[q]);
+      pb[hh] = __builtin_bit_cast(f16x8, u32x4{wh[0], wh[1], wh[2], wh[3]});
+      pl[hh] = __builtin_bit_cast(f16x8, u32x4{wl[0], wl[1], wl[2], wl[3]});
     }
     // ---- O^T += V^T P^T from the staged tile ----
     const _Float16* vtr = sv + vtr_off;
