@@ -243,8 +243,9 @@ int bc_packed_decode(bc_shape shape, const bc_half* q, const bc_half* packed_kv,
                      long long kv_stride, float scale, bc_stream_t stream);
 
 /* Bytes of workspace bc_packed_decode_ws needs for this shape: FP32
- * partials of min(R + B, 2R) slots of Hq * (D + 2) floats and one int per
- * range, R = 4 * CUs / head blocks flat ranges (twice that at dim 64, at
+ * partials of S slots of Hq * (D + 2) floats and one int per range, S = 2R
+ * above 64 sequences where R < 4B, else R + B (at most 2R either way),
+ * R = 4 * CUs / head blocks flat ranges (twice that at dim 64, at
  * most half of batch * max_pages).  0 when bc_auto_splits, given the table's
  * capacity (max_pages * 16 tokens), keeps the shape unsplit: one or two
  * head blocks whose (sequence, head block) workgroups fill the CUs; a batch
