@@ -89,6 +89,18 @@ def median_us(torch, fn, trials=7, repeats=20, warmup=5):
     return statistics.median(times)
 
 
+def paired_median_us(torch, fns, rounds=3):
+    """median_us of several calls that run the same work, taken in alternating
+    rounds (the median of each call's per-round medians), so that a drift of
+    the GPU's speed over the run (after a fixture is written, say) does not
+    favour whichever call is timed first."""
+    per = [[] for _ in fns]
+    for _ in range(rounds):
+        for i, fn in enumerate(fns):
+            per[i].append(median_us(torch, fn))
+    return [statistics.median(v) for v in per]
+
+
 def graph_replay_us(torch, make_call, out, calls=20, replays=20):
     """Per-call time of `calls` back-to-back calls captured in one HIP graph
     (torch.cuda.CUDAGraph on ROCm) and replayed `replays` times, as a serving
@@ -321,9 +333,9 @@ def bench_packed_modes(cx, p, workload):
     t = cx.torch
     res = {}
     outs = {}
-    for mode in ("ws", "reference"):
-        fn = packed_call(cx, p, mode)
-        us = median_us(t, fn)
+    modes = ("ws", "reference")
+    fns = [packed_call(cx, p, mode) for mode in modes]
+    for mode, fn, us in zip(modes, fns, paired_median_us(t, fns)):
         res[f"{mode}_us"] = round(us, 3)
         res[f"{mode}_gbs"] = round(p.bytes / us / 1e3, 1)
         fn()
@@ -485,8 +497,9 @@ def bench_tree(cx, batch, prefix, seed, with_expanded, nodes=7):
     res = {}
     calls = {"ws": tree_call(cx, f, True), "ref": tree_call(cx, f, False)}
     outs = {}
-    for name, fn in calls.items():
-        res[f"tree_{name}_us"] = round(median_us(t, fn), 3)
+    times = paired_median_us(t, list(calls.values()))
+    for (name, fn), us in zip(calls.items(), times):
+        res[f"tree_{name}_us"] = round(us, 3)
         fn()
         t.cuda.synchronize()
         outs[name] = f["out"].clone()
