@@ -385,14 +385,17 @@ def bench_c5_paged(cx, c5):
 
 def tree_setup(cx, batch, prefix, seed, nodes=7):
     """Shared-prefix tree fixture on the GPU: every request's page-table row
-    names the same physical pages (random permutation of the pool)."""
+    names the same physical pages (random permutation of the pool), and the
+    rows hold two unused entries (-1) past the prefix's pages, as the
+    reference's fixture does (src/main.cu:152-158)."""
     t = cx.torch
     rng = np.random.default_rng(seed)
     hq, hkv, d, n = 32, 8, 128, nodes
     npg = -(-prefix // PAGE)
     pool = npg + 2 * batch + 2
     perm = rng.permutation(pool).astype(np.int32)
-    pages = np.tile(perm[:npg], (batch, 1)).astype(np.int32)
+    pages = np.full((batch, npg + 2), -1, dtype=np.int32)
+    pages[:, :npg] = perm[:npg]
     parent = np.full((batch, n), -1, dtype=np.int32)
     for b in range(batch):
         for i in range(1, n):
